@@ -1,0 +1,368 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 GGML_OP_FLASH_ATTN_EXT path on one MI355X.
+
+Headline workload (the `value`): audio-encoder self-attention prefill,
+1500 frames x 20 heads, hd 64, no mask, scale 1/8, 32 layers with distinct
+synthetic N(0,1) tensors. One step = the 32 layer calls. value = algorithmic
+TFLOP/s (4*D*Hq per (q, kv) pair).
+
+Every configured shape is also measured and reported under "configs":
+decode at n_kv 1024 and 8192, decoder prefill 439 causal, the 100-step
+sliding-window decode and the 32-stream ragged batch. HBM-bound shapes rotate
+over per-layer buffers larger than the 256 MB MALL, so their bytes come from
+HBM; the sliding window is also reported warm (one cache).
+
+The CPU baseline is the ggml-faithful C restatement of the op (the oracle),
+timed on the host cores with min(hw threads, 16) threads, voxtral's default.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib.util
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense f16/bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+METRIC = "attn µs/layer; prefill TFLOP/s % MFMA peak; decode HBM GB/s % peak @1 GPU"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def load_package():
+    pkg_dir = os.path.join(ROOT, "voxtral.cpp_amd")
+    spec = importlib.util.spec_from_file_location(
+        "voxtral_cpp_amd", os.path.join(pkg_dir, "__init__.py"), submodule_search_locations=[pkg_dir])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["voxtral_cpp_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+PKG = load_package()
+vxfa, views = PKG.vxfa, PKG.views
+
+
+# ---------------------------------------------------------------------------
+# synthetic inputs on the device
+
+def randn(torch, shape, seed, sigma=1.0, dtype=None):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    if sigma != 1.0:
+        x.mul_(sigma)
+    return x.to(dtype) if dtype is not None else x
+
+
+class Layer:
+    """Descriptors of one flash_attn_ext call plus the tensors behind them."""
+
+    def __init__(self, q, k, v, mask, dst, scale, keep):
+        self.q, self.k, self.v, self.mask, self.dst = q, k, v, mask, dst
+        self.scale = scale
+        self.keep = keep
+
+
+def f32s(x):
+    import numpy as np
+    return float(np.float32(x))
+
+
+def encoder_layers(torch, n_layers, seq=1500, heads=20, hd=64, seed=1000):
+    out = []
+    for i in range(n_layers):
+        q = randn(torch, (seq, heads, hd), seed + 3 * i).half().float()  # f16-valued F32, as after mul_mat
+        k = randn(torch, (seq, heads, hd), seed + 3 * i + 1, dtype=torch.float16)
+        v = randn(torch, (seq, heads, hd), seed + 3 * i + 2, dtype=torch.float16)
+        dst = torch.empty(seq * heads * hd, device="cuda", dtype=torch.float32)
+        out.append(Layer(vxfa.desc(q.data_ptr(), vxfa.F32, *views.encoder_qkv(seq, heads, hd, 4)),
+                         vxfa.desc(k.data_ptr(), vxfa.F16, *views.encoder_qkv(seq, heads, hd, 2)),
+                         vxfa.desc(v.data_ptr(), vxfa.F16, *views.encoder_qkv(seq, heads, hd, 2)),
+                         None,
+                         vxfa.desc(dst.data_ptr(), vxfa.F32, *views.dst(hd, heads, seq)),
+                         f32s(1.0 / math.sqrt(hd)), (q, k, v, dst)))
+    return out
+
+
+def decode_layers(torch, n_layers, n_kv, hq=32, hkv=8, hd=128, capacity=None, seed=2000, batch=1,
+                  kv_sigma=1.0, masks=None):
+    cap = capacity or n_kv
+    out = []
+    for i in range(n_layers):
+        q = randn(torch, (batch, 1, hq, hd), seed + 3 * i)
+        k = randn(torch, (batch, cap, hkv, hd), seed + 3 * i + 1, kv_sigma, torch.float16)
+        v = randn(torch, (batch, cap, hkv, hd), seed + 3 * i + 2, kv_sigma, torch.float16)
+        dst = torch.empty(batch * hq * hd, device="cuda", dtype=torch.float32)
+        qne, qnb = views.decoder_q(1, hq, hd)
+        qne = (qne[0], qne[1], qne[2], batch)
+        qnb = (qnb[0], qnb[1], qnb[2], hq * hd * 4)
+        kne, knb = views.kv_cache(n_kv, hkv, hd, cap, batch=batch)
+        md = None
+        if masks is not None:
+            m = masks
+            md = vxfa.desc(m.data_ptr(), vxfa.F16, *views.mask(n_kv, 1, 1, batch))
+        out.append(Layer(vxfa.desc(q.data_ptr(), vxfa.F32, qne, qnb),
+                         vxfa.desc(k.data_ptr(), vxfa.F16, kne, knb),
+                         vxfa.desc(v.data_ptr(), vxfa.F16, kne, knb),
+                         md,
+                         vxfa.desc(dst.data_ptr(), vxfa.F32, *views.dst(hd, hq, 1, batch)),
+                         f32s(1.0 / math.sqrt(hd)), (q, k, v, dst, masks)))
+    return out
+
+
+def prefill_layers(torch, n_layers, n=439, hq=32, hkv=8, hd=128, seed=3000):
+    i_q = torch.arange(n, device="cuda")[:, None]
+    i_k = torch.arange(n, device="cuda")[None, :]
+    mask = torch.where(i_k <= i_q, 0.0, float("-inf")).to(torch.float16).contiguous()
+    out = []
+    for i in range(n_layers):
+        q = randn(torch, (n, hq, hd), seed + 3 * i)
+        k = randn(torch, (n, hkv, hd), seed + 3 * i + 1, dtype=torch.float16)
+        v = randn(torch, (n, hkv, hd), seed + 3 * i + 2, dtype=torch.float16)
+        dst = torch.empty(n * hq * hd, device="cuda", dtype=torch.float32)
+        kne, knb = views.kv_cache(n, hkv, hd, n)
+        out.append(Layer(vxfa.desc(q.data_ptr(), vxfa.F32, *views.decoder_q(n, hq, hd)),
+                         vxfa.desc(k.data_ptr(), vxfa.F16, kne, knb),
+                         vxfa.desc(v.data_ptr(), vxfa.F16, kne, knb),
+                         vxfa.desc(mask.data_ptr(), vxfa.F16, *views.mask(n, n)),
+                         vxfa.desc(dst.data_ptr(), vxfa.F32, *views.dst(hd, hq, n)),
+                         f32s(1.0 / math.sqrt(hd)), (q, k, v, dst, mask)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# timing
+
+def time_calls(torch, ctx, calls, steps, warmup):
+    """calls: list of Layer for one step. Returns (ms per step, µs per call)."""
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    def one_step():
+        for L in calls:
+            ctx.flash_attn_ext(L.q, L.k, L.v, L.mask, L.dst, L.scale, stream=sh)
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        one_step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    return ms / steps, 1000.0 * ms / (steps * len(calls))
+
+
+def decode_bytes(n_live, hq=32, hkv=8, hd=128, mask_bytes=0):
+    return n_live * hkv * hd * 2 * 2 + hq * hd * 4 * 2 + mask_bytes
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (the oracle), bounded sample
+
+def cpu_baseline_encoder(seq=1500, heads=20, hd=64):
+    """One full encoder layer through the ggml-faithful CPU restatement."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).astype(np.float32)
+    k = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
+    qv = oracle.View(q, oracle.F32, *views.encoder_qkv(seq, heads, hd, 4))
+    kv = oracle.View(k, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2))
+    vv = oracle.View(v, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2))
+    threads = oracle.default_threads()
+    oracle.fa_ggml(qv, kv, vv, None, 0.125, vkq_f16=True, threads=threads)  # warm-up (small, same code)
+    t0 = time.perf_counter()
+    oracle.fa_ggml(qv, kv, vv, None, 0.125, vkq_f16=True, threads=threads)
+    dt = time.perf_counter() - t0
+    flops = 4.0 * seq * seq * hd * heads
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"1 encoder layer (1500x1500, 20 heads, hd64) through oracle/fa_oracle.c "
+                      f"(ggml one-row algorithm, f16 V accumulation), {dt:.2f} s",
+            "us_per_layer": dt * 1e6}
+
+
+def cpu_decode_us(n_kv=8192):
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((1, 32, 128), dtype=np.float32)
+    k = rng.standard_normal((n_kv, 8, 128), dtype=np.float32).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((n_kv, 8, 128), dtype=np.float32).astype(np.float16).view(np.uint16)
+    qv = oracle.View(q, oracle.F32, *views.decoder_q(1, 32, 128))
+    kne, knb = views.kv_cache(n_kv, 8, 128, n_kv)
+    kv, vv = oracle.View(k, oracle.F16, kne, knb), oracle.View(v, oracle.F16, kne, knb)
+    threads = oracle.default_threads()
+    oracle.fa_ggml(qv, kv, vv, None, f32s(1 / math.sqrt(128)), vkq_f16=True, threads=threads)
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.fa_ggml(qv, kv, vv, None, f32s(1 / math.sqrt(128)), vkq_f16=True, threads=threads)
+    return (time.perf_counter() - t0) / reps * 1e6, threads
+
+
+# ---------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma list of configs to run (debug)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(attention shards by kv head or stream with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    vxfa.load()
+    ctx = vxfa.Context(0)
+    only = set(args.only.split(",")) if args.only else None
+    want = lambda name: only is None or name in only
+    K, W = args.steps, args.warmup
+    configs = {}
+
+    # --- headline: encoder prefill, 32 layers ---
+    enc = encoder_layers(torch, 32)
+    flops_enc = 4.0 * 1500 * 1500 * 64 * 20
+    ms_step, us_layer = time_calls(torch, ctx, enc, K, W)
+    tflops = flops_enc / (us_layer * 1e-6) / 1e12
+    log(f"[encoder] {us_layer:.2f} us/layer  {tflops:.1f} TFLOP/s")
+    configs["encoder_prefill_1500x20_hd64"] = {
+        "us_per_layer": us_layer, "tflops": tflops, "frac_mfma_peak": tflops / MFMA_PEAK_TFLOPS,
+        "flops_per_layer": flops_enc, "layers": 32}
+    headline = (ms_step, us_layer, tflops)
+    del enc
+    torch.cuda.empty_cache()
+
+    if want("decode"):
+        for n_kv, layers in ((1024, 30), (8192, 30)):
+            dl = decode_layers(torch, layers, n_kv, seed=2000 + n_kv)
+            _, us = time_calls(torch, ctx, dl, K, W)
+            by = decode_bytes(n_kv)
+            gbs = by / (us * 1e-6) / 1e9
+            log(f"[decode n_kv={n_kv}] {us:.2f} us/layer  {gbs:.0f} GB/s")
+            configs[f"decode_nkv{n_kv}"] = {"us_per_layer": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                                            "bytes_per_layer": by, "layers": layers, "cache": "cold (30 layers)"}
+            del dl
+            torch.cuda.empty_cache()
+
+    if want("prefill"):
+        pl = prefill_layers(torch, 30)
+        _, us = time_calls(torch, ctx, pl, K, W)
+        fl = 4.0 * 128 * 32 * (439 * 440 // 2)
+        tf = fl / (us * 1e-6) / 1e12
+        log(f"[decoder prefill 439 causal] {us:.2f} us/layer  {tf:.1f} TFLOP/s")
+        configs["decoder_prefill_439_causal"] = {"us_per_layer": us, "tflops": tf,
+                                                 "frac_mfma_peak": tf / MFMA_PEAK_TFLOPS,
+                                                 "flops_per_layer": fl, "layers": 30}
+        del pl
+        torch.cuda.empty_cache()
+
+    if want("sliding"):
+        cap, n0, window, steps = 16384, 16284, 2048, 100
+        res = {}
+        for mode, ncache in (("cold", 8), ("warm", 1)):
+            caches = decode_layers(torch, ncache, cap, capacity=cap, seed=4000)
+            masks = []
+            calls = []
+            for t in range(steps):
+                n_kv = n0 + t + 1
+                m = torch.zeros(n_kv, device="cuda", dtype=torch.float16)
+                m[: n_kv - window] = float("-inf")
+                masks.append(m)
+                L = caches[t % ncache]
+                kne, knb = views.kv_cache(n_kv, 8, 128, cap)
+                calls.append(Layer(L.q, vxfa.desc(L.k.data, vxfa.F16, kne, knb),
+                                   vxfa.desc(L.v.data, vxfa.F16, kne, knb),
+                                   vxfa.desc(m.data_ptr(), vxfa.F16, *views.mask(n_kv, 1)), L.dst, L.scale, None))
+            _, us = time_calls(torch, ctx, calls, max(1, K // 4), 1)
+            by = decode_bytes(window, mask_bytes=2 * (n0 + steps // 2))
+            res[mode] = (us, by / (us * 1e-6) / 1e9)
+            del caches, calls, masks
+            torch.cuda.empty_cache()
+        log(f"[sliding window] cold {res['cold'][0]:.2f} us/step {res['cold'][1]:.0f} GB/s; "
+            f"warm {res['warm'][0]:.2f} us/step")
+        configs["sliding_window_decode_16k_w2048"] = {
+            "us_per_step_cold": res["cold"][0], "gbs_cold": res["cold"][1],
+            "frac_hbm_peak_cold": res["cold"][1] / HBM_PEAK_GBS,
+            "us_per_step_warm": res["warm"][0], "gbs_warm": res["warm"][1], "steps": steps,
+            "bytes_per_step": decode_bytes(window, mask_bytes=2 * (n0 + steps // 2))}
+
+    if want("batched"):
+        B, cap = 32, 8192
+        g = torch.Generator(device="cpu")
+        g.manual_seed(5)
+        lens = torch.randint(512, 8193, (B,), generator=g)
+        mask = torch.zeros(B, cap, dtype=torch.float16)
+        for b in range(B):
+            mask[b, lens[b]:] = float("-inf")
+        mask = mask.cuda()
+        bl = decode_layers(torch, 1, cap, batch=B, seed=5000, kv_sigma=0.5, masks=mask)
+        _, us = time_calls(torch, ctx, bl, K, W)
+        by = int(lens.sum()) * 8 * 128 * 2 * 2 + B * cap * 2 + B * 32 * 128 * 4 * 2
+        gbs = by / (us * 1e-6) / 1e9
+        log(f"[batched 32 streams] {us:.2f} us/call {gbs:.0f} GB/s")
+        configs["batched_ragged_32_streams"] = {"us_per_call": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                                                "bytes_per_call": by, "sum_len": int(lens.sum())}
+        del bl
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("[cpu baseline] encoder layer on host cores ...")
+        cpu = cpu_baseline_encoder()
+        us_cpu_dec, thr = cpu_decode_us(8192)
+        configs.setdefault("decode_nkv8192", {})["cpu_us_per_layer"] = us_cpu_dec
+        configs["encoder_prefill_1500x20_hd64"]["cpu_us_per_layer"] = cpu.pop("us_per_layer")
+        log(f"[cpu baseline] {cpu['value']*1e3:.2f} GFLOP/s encoder, decode 8192 {us_cpu_dec:.0f} us, {thr} threads")
+
+    ms_step, us_layer, tflops = headline
+    line = {
+        "metric": METRIC,
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic, seeded N(0,1) (torch generator on device)",
+        "config": {"workload": "audio-encoder self-attention prefill: q/k/v [64, 1500, 20] (q f16-valued F32, "
+                               "k/v f16), no mask, scale 1/8, 32 layers per step",
+                   "global_batch": 1, "seq_len": 1500, "heads": 20, "head_dim": 64, "layers": 32},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "fa_prefill_kernel<64,4,false>", "us_per_launch": us_layer},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,120 @@
+/*
+ * vxfa.h — C ABI of the MI355X (gfx950) attention path for voxtral.cpp.
+ *
+ * One operation: GGML_OP_FLASH_ATTN_EXT, with ggml's tensor contract.
+ *
+ *   dst = softmax(scale * Q K^T + mask) V, per query head, GQA-broadcast K/V.
+ *
+ * voxtral.cpp emits this op at two sites:
+ *   src/voxtral.cpp:1611  encoder self-attention   (hd 64, no mask offline)
+ *   src/voxtral.cpp:1802  decoder GQA attention    (32 q / 8 kv heads, hd 128,
+ *                                                  causal mask or none)
+ * Both pass max_bias = 0 and logit_softcap = 0.
+ * The op constructor is ggml_flash_attn_ext(ctx, q, k, v, mask, scale,
+ * max_bias, logit_softcap). It lives in ggml (external, pinned in
+ * CMakeLists.txt:36-39). It is executed by a ggml backend's graph_compute,
+ * which the scheduler calls from src/voxtral.cpp:2097, 2193, 2382.
+ *
+ * Tensor contract (ggml order, ne[0] fastest, nb in bytes):
+ *   q    [D,  Nq,  Hq,  B ]  F32 or F16, rows contiguous (nb[0] = elt size)
+ *   k    [D,  Nkv, Hkv, Bk]  F16, rows contiguous
+ *   v    [D,  Nkv, Hkv, Bk]  F16, rows contiguous (not transposed)
+ *   mask [Nkv, >=Nq, Hm, Bm] F16 additive (0 / -inf in voxtral), nullable,
+ *                            elements contiguous along ne[0]
+ *   dst  [D,  Hq,  Nq,  B ]  F32, contiguous (permuted relative to q)
+ * with Hq % Hkv == 0, B % Bk == 0, Hq % Hm == 0, B % Bm == 0.
+ * Query head h reads kv head h / (Hq / Hkv) and mask plane h % Hm.
+ *
+ * Semantics follow ggml's CPU kernel: a mask entry of -inf removes that kv
+ * position; a query row with every position removed produces zeros.
+ *
+ * Everything here is plain C: pointers, sizes and status codes. No HIP or
+ * torch types cross the boundary. The stream argument is a hipStream_t
+ * passed as void* (NULL = the null stream).
+ */
+#ifndef VXFA_H
+#define VXFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. The numeric values equal ggml's GGML_TYPE_F32 / GGML_TYPE_F16,
+ * so a ggml backend can pass tensor->type through unchanged. */
+enum vxfa_type {
+    VXFA_TYPE_F32 = 0,
+    VXFA_TYPE_F16 = 1,
+};
+
+/* Status codes. Nothing aborts and no C++ exception crosses the ABI.
+ * VXFA_UNSUPPORTED plays the role of ggml's supports_op() == false: the
+ * caller runs the op elsewhere (ggml's scheduler falls back to the CPU
+ * backend, which voxtral lists last at src/voxtral.cpp:1167-1170). */
+enum vxfa_status {
+    VXFA_OK           = 0,
+    VXFA_UNSUPPORTED  = 1,  /* valid op, but this path does not implement it  */
+    VXFA_INVALID_ARG  = 2,  /* violates the ggml contract (shapes, strides)   */
+    VXFA_NO_WORKSPACE = 3,  /* could not allocate the split-KV workspace      */
+    VXFA_HIP_ERROR    = 4,  /* a HIP call failed; see vxfa_last_error()       */
+};
+
+/* A ggml tensor view: exactly the fields of struct ggml_tensor that the op
+ * reads (type, ne, nb, data). data is a device pointer. */
+typedef struct vxfa_tensor {
+    void*   data;
+    int32_t type;   /* enum vxfa_type */
+    int32_t pad_;   /* keep ne[] 8-byte aligned; ignored */
+    int64_t ne[4];
+    size_t  nb[4];
+} vxfa_tensor;
+
+/* Per-stream context. Owns the split-KV workspace (partial O, running max
+ * and sum per split, plus arrival counters) and grows it on demand; the
+ * caller's tensors are never allocated or freed here. One context per
+ * stream; calls on one context must not overlap. */
+typedef struct vxfa_ctx vxfa_ctx;
+
+/* Create a context bound to HIP device `device`. Returns NULL on failure. */
+vxfa_ctx* vxfa_ctx_create(int device);
+
+/* Destroy a context and free its workspace. NULL is accepted. */
+void vxfa_ctx_destroy(vxfa_ctx* ctx);
+
+/* Capability check. Mirrors a ggml backend's supports_op() for
+ * GGML_OP_FLASH_ATTN_EXT (the scheduler consults it when placing the node;
+ * placement order is set at src/voxtral.cpp:1156-1175). Pure host code: it
+ * only reads the descriptors, never dereferences data, and makes no HIP call,
+ * so it runs on a machine without a GPU.
+ * Returns VXFA_OK, VXFA_UNSUPPORTED or VXFA_INVALID_ARG. */
+int vxfa_supports(const vxfa_tensor* q, const vxfa_tensor* k,
+                  const vxfa_tensor* v, const vxfa_tensor* mask,
+                  const vxfa_tensor* dst, float scale, float max_bias,
+                  float logit_softcap);
+
+/* Execute GGML_OP_FLASH_ATTN_EXT. Replaces the backend kernel behind
+ * ggml_flash_attn_ext(ctx, q, k, v, mask, scale, max_bias, logit_softcap)
+ * at src/voxtral.cpp:1611 and :1802. Asynchronous on `stream`: the call
+ * returns after the launches are queued. Output is deterministic for equal
+ * inputs (fixed split boundaries and combine order). */
+int vxfa_flash_attn_ext(vxfa_ctx* ctx, const vxfa_tensor* q,
+                        const vxfa_tensor* k, const vxfa_tensor* v,
+                        const vxfa_tensor* mask, vxfa_tensor* dst, float scale,
+                        float max_bias, float logit_softcap, void* stream);
+
+/* Human-readable name of a status code (static storage). */
+const char* vxfa_status_str(int status);
+
+/* Message for the last failing call on this context ("" if none). */
+const char* vxfa_last_error(const vxfa_ctx* ctx);
+
+/* Library version: major * 10000 + minor * 100 + patch. */
+int vxfa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VXFA_H */

@@ -1,0 +1,173 @@
+"""Seeded attention inputs laid out exactly as voxtral.cpp lays them out.
+
+A Case holds contiguous host buffers (numpy) and, per operand, the ggml view
+(type, ne, nb, byte offset) into one of them. The same bytes go to the oracle
+(host) and, in GPU tests, to the device, so both see identical inputs.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from conftest import load_package
+from oracle.oracle import F16, F32, View
+
+views = load_package().views
+
+NEG_INF_F16 = np.uint16(0xFC00)
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def f32(x: float) -> float:
+    """ggml stores the scale as a float op param; keep it float32-exact."""
+    return float(np.float32(x))
+
+
+def normal(rng, shape, sigma=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(np.float32)
+
+
+@dataclass
+class Case:
+    name: str
+    scale: float
+    bufs: dict = field(default_factory=dict)       # name -> contiguous np.ndarray
+    views: dict = field(default_factory=dict)      # role -> (buf, type, ne, nb, offset)
+    meta: dict = field(default_factory=dict)
+
+    def add(self, role, buf_name, arr, type_, ne, nb, offset=0):
+        if buf_name not in self.bufs:
+            self.bufs[buf_name] = np.ascontiguousarray(arr)
+        self.views[role] = (buf_name, type_, tuple(ne), tuple(nb), offset)
+
+    def has(self, role):
+        return role in self.views
+
+    def oracle_view(self, role):
+        if role not in self.views:
+            return None
+        b, t, ne, nb, off = self.views[role]
+        return View(self.bufs[b], t, ne, nb, off)
+
+    @property
+    def out_shape(self):
+        _, _, qne, _, _ = self.views["q"]
+        _, _, vne, _, _ = self.views["v"]
+        return (qne[3], qne[1], qne[2], vne[0])  # [B, Nq, Hq, D]
+
+    def dst_ne_nb(self):
+        B, Nq, Hq, D = self.out_shape
+        return views.dst(D, Hq, Nq, B)
+
+
+# ---------------------------------------------------------------------------
+# builders for the shapes voxtral.cpp produces
+
+
+def decode_case(n_kv, hq=32, hkv=8, hd=128, capacity=None, seed=1, q_sigma=1.0, kv_sigma=1.0,
+                batch=1, window=None, name=None, q_f16=False):
+    """Single-token decode against a token-major f16 cache (src/voxtral.cpp:1736-1805).
+    window: if set, additive mask [n_kv, 1] with -inf outside the last `window` rows."""
+    rng = np.random.default_rng(seed)
+    cap = capacity or n_kv
+    c = Case(name or f"decode_nkv{n_kv}_b{batch}", f32(1.0 / math.sqrt(hd)))
+    q = normal(rng, (batch, 1, hq, hd), q_sigma)
+    if q_f16:
+        c.add("q", "q", f16_bits(q), F16, *_batched_q(1, hq, hd, 2, batch))
+    else:
+        c.add("q", "q", q, F32, *_batched_q(1, hq, hd, 4, batch))
+    k = f16_bits(normal(rng, (batch, cap, hkv, hd), kv_sigma))
+    v = f16_bits(normal(rng, (batch, cap, hkv, hd), kv_sigma))
+    ne, nb = views.kv_cache(n_kv, hkv, hd, cap, batch=batch)
+    c.add("k", "k", k, F16, ne, nb)
+    c.add("v", "v", v, F16, ne, nb)
+    if window is not None:
+        m = np.zeros((batch, 1, n_kv), dtype=np.uint16)
+        m[:, :, : max(0, n_kv - window)] = NEG_INF_F16
+        c.add("mask", "mask", m, F16, *views.mask(n_kv, 1, 1, batch))
+    return c
+
+
+def _batched_q(n_tokens, heads, hd, elt, batch):
+    ne, nb = views.decoder_q(n_tokens, heads, hd, elt)
+    return (ne[0], ne[1], ne[2], batch), (nb[0], nb[1], nb[2], n_tokens * heads * hd * elt)
+
+
+def encoder_case(seq=1500, heads=20, hd=64, seed=2, name=None, window=None):
+    """Encoder self-attention (src/voxtral.cpp:1580-1613): q/k/v [hd, seq, heads]
+    views of [seq][heads][hd] buffers. q is f16-valued, stored as F32 (the
+    reference's q is a mul_mat output); window: realtime sliding-causal mask
+    (src/voxtral.cpp:2179-2190)."""
+    rng = np.random.default_rng(seed)
+    c = Case(name or f"encoder_seq{seq}", f32(1.0 / math.sqrt(hd)))
+    qh = f16_bits(normal(rng, (seq, heads, hd)))
+    q = qh.view(np.float16).astype(np.float32)
+    k = f16_bits(normal(rng, (seq, heads, hd)))
+    v = f16_bits(normal(rng, (seq, heads, hd)))
+    c.add("q", "q", q, F32, *views.encoder_qkv(seq, heads, hd, 4))
+    c.add("k", "k", k, F16, *views.encoder_qkv(seq, heads, hd, 2))
+    c.add("v", "v", v, F16, *views.encoder_qkv(seq, heads, hd, 2))
+    if window is not None:
+        qi = np.arange(seq)[:, None]
+        ki = np.arange(seq)[None, :]
+        allow = (ki <= qi) & (ki >= qi - (window - 1))
+        m = np.where(allow, np.uint16(0), NEG_INF_F16).astype(np.uint16)
+        c.add("mask", "mask", m, F16, *views.mask(seq, seq))
+    return c
+
+
+def prefill_case(n=439, hq=32, hkv=8, hd=128, seed=3, causal=True, kv_offset=0, capacity=None, name=None):
+    """Decoder prefill (src/voxtral.cpp:1736-1805) with the causal mask of
+    fill_causal_mask (:2104-2111); kv_offset > 0 gives n_kv = kv_offset + n."""
+    rng = np.random.default_rng(seed)
+    n_kv = kv_offset + n
+    cap = capacity or n_kv
+    c = Case(name or f"prefill_n{n}_off{kv_offset}", f32(1.0 / math.sqrt(hd)))
+    q = normal(rng, (n, hq, hd))
+    c.add("q", "q", q, F32, *views.decoder_q(n, hq, hd))
+    k = f16_bits(normal(rng, (cap, hkv, hd)))
+    v = f16_bits(normal(rng, (cap, hkv, hd)))
+    ne, nb = views.kv_cache(n_kv, hkv, hd, cap)
+    c.add("k", "k", k, F16, ne, nb)
+    c.add("v", "v", v, F16, ne, nb)
+    if causal:
+        qi = np.arange(n)[:, None] + kv_offset
+        ki = np.arange(n_kv)[None, :]
+        m = np.where(ki <= qi, np.uint16(0), NEG_INF_F16).astype(np.uint16)
+        c.add("mask", "mask", m, F16, *views.mask(n_kv, n))
+    return c
+
+
+def batched_case(n_streams=32, hq=32, hkv=8, hd=128, capacity=8192, lo=512, hi=8192, seed=5,
+                 kv_sigma=0.5, name=None):
+    """32 independent decode streams along ne[3] with ragged valid lengths
+    drawn from U{lo..hi} and a per-stream length mask [cap, 1, 1, B]."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, size=n_streams)
+    c = decode_case(capacity, hq, hkv, hd, capacity=capacity, seed=seed + 1000, kv_sigma=kv_sigma,
+                    batch=n_streams, name=name or f"batched_{n_streams}")
+    m = np.zeros((n_streams, 1, capacity), dtype=np.uint16)
+    for b, L in enumerate(lens):
+        m[b, 0, L:] = NEG_INF_F16
+    c.add("mask", "mask", m, F16, *views.mask(capacity, 1, 1, n_streams))
+    c.meta["lens"] = lens
+    return c
+
+
+def oracle_ggml(c: Case, vkq_f16=False, flags=0, threads=None):
+    """ggml-faithful restatement; fp32 V accumulation unless vkq_f16 (the one-row
+    kernel's f16 accumulator, used as the bracket)."""
+    from oracle import oracle
+    return oracle.fa_ggml(c.oracle_view("q"), c.oracle_view("k"), c.oracle_view("v"), c.oracle_view("mask"),
+                          c.scale, vkq_f16=vkq_f16, flags=flags, threads=threads)
+
+
+def oracle_f64(c: Case, threads=None):
+    from oracle import oracle
+    return oracle.fa_f64(c.oracle_view("q"), c.oracle_view("k"), c.oracle_view("v"), c.oracle_view("mask"),
+                         c.scale, threads=threads)

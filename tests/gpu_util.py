@@ -1,0 +1,62 @@
+"""Device side of the parity tests: copy a Case's host bytes to the GPU, call
+the C ABI through ctypes, read the output back. Inputs on the device are
+byte-identical to what the oracle reads."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from conftest import load_package
+
+vxfa = load_package().vxfa
+
+CANARY = 4096  # floats of guard band on each side of dst
+CANARY_BITS = np.uint32(0x7FC0DEAD)  # a NaN payload the kernels never write
+
+
+def to_device(case):
+    return {n: torch.from_numpy(a.view(np.uint8).reshape(-1)).to("cuda") for n, a in case.bufs.items()}
+
+
+def descs(case, dev):
+    out = {}
+    for role, (b, t, ne, nb, off) in case.views.items():
+        out[role] = vxfa.desc(dev[b].data_ptr() + off, t, ne, nb)
+    return out
+
+
+class Runner:
+    """Owns one vxfa context on the current torch stream."""
+
+    def __init__(self):
+        self.ctx = vxfa.Context(0)
+
+    def run(self, case, dev=None, check=True):
+        dev = dev if dev is not None else to_device(case)
+        d = descs(case, dev)
+        B, Nq, Hq, D = case.out_shape
+        n = B * Nq * Hq * D
+        buf = torch.from_numpy(np.full(n + 2 * CANARY, CANARY_BITS, dtype=np.uint32)).to("cuda")
+        ne, nb = case.dst_ne_nb()
+        dst = vxfa.desc(buf.data_ptr() + 4 * CANARY, vxfa.F32, ne, nb)
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = self.ctx.flash_attn_ext(d["q"], d["k"], d["v"], d.get("mask"), dst, case.scale,
+                                     stream=stream, check=check)
+        torch.cuda.synchronize()
+        host = buf.cpu().numpy()
+        assert (host[:CANARY] == CANARY_BITS).all(), "write before dst"
+        assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
+        return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy()
+
+    def close(self):
+        self.ctx.close()
+
+
+def parity(gpu, ref, atol=2e-3, rtol=1e-2):
+    """max-abs and relative (Frobenius) error of gpu against ref."""
+    ref = ref.astype(np.float64)
+    diff = gpu.astype(np.float64) - ref
+    maxabs = float(np.abs(diff).max()) if diff.size else 0.0
+    den = float(np.linalg.norm(ref))
+    rel = float(np.linalg.norm(diff) / den) if den > 0 else float(np.linalg.norm(diff))
+    return maxabs, rel, (maxabs <= atol and rel <= rtol)

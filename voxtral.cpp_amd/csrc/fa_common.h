@@ -1,0 +1,87 @@
+// fa_common.h — shared device helpers and launch descriptors for the gfx950
+// attention kernels. CDNA4 only: 64-lane wavefronts, MFMA f16 tiles, LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vxfa {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr uint16_t kF16NegInf = 0xFC00u;
+
+// Everything a kernel needs from the ggml descriptors, in elements where the
+// row is contiguous and in bytes for the outer strides.
+struct AttnArgs {
+    const void* q;        // F32 or F16
+    const _Float16* k;
+    const _Float16* v;
+    const uint16_t* mask; // F16 bits, may be null
+    float* dst;           // [B][Nq][Hq][D]
+    float* ws;            // split-KV partials (decode)
+    uint32_t* counters;   // split-KV arrival counters (decode), self-resetting
+    int64_t q_nb1, q_nb2, q_nb3;   // bytes
+    int64_t k_nb1, k_nb2, k_nb3;   // bytes
+    int64_t v_nb1, v_nb2, v_nb3;   // bytes
+    int64_t m_nb1, m_nb2, m_nb3;   // bytes
+    int32_t nq, nkv, hq, hkv, b, bk, hm, bm;
+    int32_t q_f16;        // q element type is f16
+    int32_t n_split;      // decode: workgroups per (batch, kv head)
+    float scale_log2;     // scale * log2(e)
+};
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// Load 8 consecutive Q elements (F32 or F16) and round them to f16 (RNE),
+// the conversion ggml applies to Q before an f16 K dot product.
+__device__ __forceinline__ half8 load_q8(const void* base, int64_t byte_off, bool q_f16) {
+    half8 r;
+    if (q_f16) {
+        r = *(const half8*)((const char*)base + byte_off);
+    } else {
+        const floatx4* p = (const floatx4*)((const char*)base + byte_off);
+        floatx4 a = p[0], c = p[1];
+        r[0] = (_Float16)a[0]; r[1] = (_Float16)a[1]; r[2] = (_Float16)a[2]; r[3] = (_Float16)a[3];
+        r[4] = (_Float16)c[0]; r[5] = (_Float16)c[1]; r[6] = (_Float16)c[2]; r[7] = (_Float16)c[3];
+    }
+    return r;
+}
+
+// Cross-lane helpers over a 64-lane wavefront.
+__device__ __forceinline__ float shfl_xor(float x, int m) { return __shfl_xor(x, m, 64); }
+
+// max / sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15)
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, shfl_xor(x, 8));
+    x = fmaxf(x, shfl_xor(x, 4));
+    x = fmaxf(x, shfl_xor(x, 2));
+    x = fmaxf(x, shfl_xor(x, 1));
+    return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += shfl_xor(x, 8);
+    x += shfl_xor(x, 4);
+    x += shfl_xor(x, 2);
+    x += shfl_xor(x, 1);
+    return x;
+}
+
+}  // namespace vxfa
+
+// Host-side launchers (implemented in the kernel translation units).
+namespace vxfa {
+hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t stream);
+hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
+hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
+}  // namespace vxfa

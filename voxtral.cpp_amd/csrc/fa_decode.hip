@@ -1,0 +1,335 @@
+// fa_decode.hip — single-query (decode-step) attention against an f16 KV
+// cache, split over the KV length, for gfx950.
+//
+// Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the decode calls
+// voxtral.cpp makes from build_decoder_layer (src/voxtral.cpp:1802) with
+// n_tokens = 1 (step graphs :1959-1962 and :2050-2053), where every KV head
+// serves G = Hq / Hkv query heads (32 / 8 = 4).
+//
+// Work decomposition
+//   grid  = (n_split, Hkv, B): one workgroup per (split of the live KV range,
+//           kv head, batch row); 4 wavefronts per workgroup.
+//   Each wavefront walks 32-position tiles of its workgroup's range.
+//   QK^T  : one v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims). The A
+//           operand holds the G query heads replicated 16/G times, so every
+//           lane receives the scores of all G heads for one position and no
+//           cross-lane reduction is needed for the dot products.
+//   K     : loaded straight from HBM into the MFMA B-operand layout
+//           (16 positions x 64 contiguous bytes per instruction, 128-bit).
+//   V     : loaded with 16 (hd128) or 8 (hd64) lanes per 256/128-byte row,
+//           fully coalesced 128-bit loads; P.V on the VALU with fp32
+//           accumulators (each lane owns 8 dims of all G heads).
+//   Softmax: fp32, exp2 with scale*log2(e) folded in, running max per head
+//           shared by the wavefront.
+//   Combine: wavefronts merge through LDS; with n_split > 1 each workgroup
+//           writes (O, m, l) for its split and the last workgroup to arrive
+//           (atomic counter, reset by that workgroup) merges all splits in a
+//           fixed order, so the output does not depend on arrival order.
+// Masks: an additive F16 mask is honoured exactly (-inf removes a position).
+// The workgroup first scans the mask row to find the live range, so a
+// sliding window or a ragged length only costs the live positions.
+#include "fa_common.h"
+
+namespace vxfa {
+
+constexpr int DEC_WAVES = 4;
+constexpr int DEC_THREADS = 64 * DEC_WAVES;
+constexpr int DEC_TILE = 32;
+constexpr int DEC_MAX_SPLIT = 64;
+
+template <int D, int G>
+__global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
+    static_assert(D == 64 || D == 128, "head dim");
+    static_assert(G == 1 || G == 2 || G == 4, "GQA group");
+    constexpr int KS = D / 32;        // MFMA k-steps of 32 dims
+    constexpr int CH = D / 8;         // 16-byte chunks per row = PV lanes per row
+    constexpr int RPI = 64 / CH;      // rows covered by one PV load instruction
+    constexpr int NV = DEC_TILE / RPI;
+
+    __shared__ floatx4 lds_p[DEC_WAVES][DEC_TILE];
+    __shared__ float lds_acc[DEC_WAVES][G][D];
+    __shared__ float lds_m[DEC_WAVES][G];
+    __shared__ float lds_l[DEC_WAVES][G];
+    __shared__ int lds_lo[DEC_WAVES], lds_hi[DEC_WAVES];
+    __shared__ int lds_last;
+    __shared__ float cw[DEC_MAX_SPLIT * G];
+    __shared__ float cM[G], cL[G];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int split = blockIdx.x;
+    const int g = blockIdx.y;
+    const int b = blockIdx.z;
+    const int bkv = b / (a.b / a.bk);
+
+    // ---- live range of the KV axis -------------------------------------
+    int lo = 0, hi = a.nkv;
+    if (a.mask) {
+        int tlo = 0x7fffffff, thi = -1;
+        const int nplanes = (a.hm == 1) ? 1 : G;
+        for (int j = 0; j < nplanes; ++j) {
+            const int hq = g * G + j;
+            const uint16_t* mrow = (const uint16_t*)((const char*)a.mask +
+                                                     (int64_t)(hq % a.hm) * a.m_nb2 +
+                                                     (int64_t)(b % a.bm) * a.m_nb3);
+            for (int i = tid; i < a.nkv; i += DEC_THREADS) {
+                if (mrow[i] != kF16NegInf) {
+                    tlo = min(tlo, i);
+                    thi = max(thi, i);
+                }
+            }
+        }
+        for (int off = 32; off >= 1; off >>= 1) {
+            tlo = min(tlo, __shfl_xor(tlo, off, 64));
+            thi = max(thi, __shfl_xor(thi, off, 64));
+        }
+        if (lane == 0) { lds_lo[wave] = tlo; lds_hi[wave] = thi; }
+        __syncthreads();
+        tlo = lds_lo[0]; thi = lds_hi[0];
+        for (int w = 1; w < DEC_WAVES; ++w) { tlo = min(tlo, lds_lo[w]); thi = max(thi, lds_hi[w]); }
+        if (thi < 0) { lo = 0; hi = 0; } else { lo = tlo; hi = thi + 1; }
+    }
+
+    const int span = hi - lo;
+    const int ntiles = (span + DEC_TILE - 1) / DEC_TILE;
+    const int t_begin = (int)(((int64_t)ntiles * split) / a.n_split);
+    const int t_end = (int)(((int64_t)ntiles * (split + 1)) / a.n_split);
+
+    // ---- Q operand: A[m][k], m = lane & 15 -> head (m % G), k-chunk lane >> 4
+    const int qelt = a.q_f16 ? 2 : 4;
+    half8 qa[KS];
+    {
+        const int hq = g * G + ((lane & 15) % G);
+        const int64_t qoff = (int64_t)hq * a.q_nb2 + (int64_t)b * a.q_nb3;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            qa[ks] = load_q8(a.q, qoff + (int64_t)(32 * ks + 8 * (lane >> 4)) * qelt, a.q_f16 != 0);
+    }
+
+    const char* kb = (const char*)a.k + (int64_t)g * a.k_nb2 + (int64_t)bkv * a.k_nb3;
+    const char* vb = (const char*)a.v + (int64_t)g * a.v_nb2 + (int64_t)bkv * a.v_nb3;
+    const uint16_t* mplane[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (a.mask) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hq = g * G + (i % G);
+            mplane[i] = (const uint16_t*)((const char*)a.mask + (int64_t)(hq % a.hm) * a.m_nb2 +
+                                          (int64_t)(b % a.bm) * a.m_nb3);
+        }
+    }
+
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
+    float acc[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
+
+    const int kcol = 8 * (lane >> 4);     // dims owned in the K operand
+    const int vrow = lane / CH;           // row offset owned in the V layout
+    const int vcol = (lane % CH) * 8;     // dims owned in the V layout
+
+    for (int t = t_begin + wave; t < t_end; t += DEC_WAVES) {
+        const int p0 = lo + t * DEC_TILE;
+        const int pend = min(p0 + DEC_TILE, hi);
+
+        half8 kr[2][KS];
+#pragma unroll
+        for (int grp = 0; grp < 2; ++grp) {
+            const int pos = min(p0 + 16 * grp + (lane & 15), pend - 1);
+            const char* kp = kb + (int64_t)pos * a.k_nb1 + kcol * 2;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) kr[grp][ks] = *(const half8*)(kp + 64 * ks);
+        }
+        half8 vr[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int pos = min(p0 + vrow + i * RPI, pend - 1);
+            vr[i] = *(const half8*)(vb + (int64_t)pos * a.v_nb1 + vcol * 2);
+        }
+
+        floatx4 sc[2];
+#pragma unroll
+        for (int grp = 0; grp < 2; ++grp) {
+            sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kr[grp][ks], sc[grp], 0, 0, 0);
+        }
+
+        // scores in log2 units; lane holds heads i (= row 4*(lane>>4)+i mod G) at its position
+        float x[2][4];
+#pragma unroll
+        for (int grp = 0; grp < 2; ++grp) {
+            const int pos = p0 + 16 * grp + (lane & 15);
+            const bool valid = pos < pend;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float mv = 0.f;
+                if (a.mask && valid) mv = f16_bits_to_f32(mplane[i][pos]) * kLog2e;
+                x[grp][i] = valid ? fmaf(sc[grp][i], a.scale_log2, mv) : -INFINITY;
+            }
+        }
+
+        float alpha[4], p[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float mx = row16_max(fmaxf(x[0][i], x[1][i]));
+            const float mnew = fmaxf(m_run[i], mx);
+            const float msafe = (mnew == -INFINITY) ? 0.f : mnew;
+            alpha[i] = exp2_fast(m_run[i] - msafe);
+            p[0][i] = exp2_fast(x[0][i] - msafe);
+            p[1][i] = exp2_fast(x[1][i] - msafe);
+            l_run[i] = fmaf(l_run[i], alpha[i], p[0][i] + p[1][i]);
+            m_run[i] = mnew;
+        }
+
+        if ((lane >> 4) == 0) {
+            lds_p[wave][lane] = floatx4{p[0][0], p[0][1], p[0][2], p[0][3]};
+            lds_p[wave][16 + lane] = floatx4{p[1][0], p[1][1], p[1][2], p[1][3]};
+        }
+        __builtin_amdgcn_wave_barrier();
+
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] *= alpha[h];
+
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const floatx4 pv = lds_p[wave][vrow + i * RPI];
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pv[h], (float)vr[i][j], acc[h][j]);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---- merge lanes, then wavefronts ------------------------------------
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float s = acc[h][j];
+#pragma unroll
+            for (int m = CH; m < 64; m <<= 1) s += shfl_xor(s, m);
+            acc[h][j] = s;
+        }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l_run[i] = row16_sum(l_run[i]);
+
+    if (lane < CH) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) lds_acc[wave][h][lane * 8 + j] = acc[h][j];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) { lds_m[wave][h] = m_run[h]; lds_l[wave][h] = l_run[h]; }
+    }
+    __syncthreads();
+
+    const int pair = b * a.hkv + g;
+    float* rec = a.ws + ((int64_t)pair * a.n_split + split) * (G * (D + 2));
+    for (int o = tid; o < G * D; o += DEC_THREADS) {
+        const int h = o / D, d = o % D;
+        float M = lds_m[0][h];
+#pragma unroll
+        for (int w = 1; w < DEC_WAVES; ++w) M = fmaxf(M, lds_m[w][h]);
+        const float Ms = (M == -INFINITY) ? 0.f : M;
+        float s = 0.f, L = 0.f;
+#pragma unroll
+        for (int w = 0; w < DEC_WAVES; ++w) {
+            const float wt = exp2_fast(lds_m[w][h] - Ms);
+            s = fmaf(wt, lds_acc[w][h][d], s);
+            L = fmaf(wt, lds_l[w][h], L);
+        }
+        if (a.n_split == 1) {
+            a.dst[((int64_t)b * a.hq + g * G + h) * D + d] = (L == 0.f) ? 0.f : s / L;
+        } else {
+            rec[o] = s;
+            if (d == 0) { rec[G * D + h] = M; rec[G * D + G + h] = L; }
+        }
+    }
+    if (a.n_split == 1) return;
+
+    // ---- split combine by the last workgroup of this (batch, kv head) ----
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = atomicAdd(&a.counters[pair], 1u);
+        lds_last = (prev == (unsigned)(a.n_split - 1));
+    }
+    __syncthreads();
+    if (!lds_last) return;
+    __threadfence();
+
+    const float* base = a.ws + (int64_t)pair * a.n_split * (G * (D + 2));
+    const int rs = G * (D + 2);
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, base[(int64_t)s * rs + G * D + tid]);
+        cM[tid] = M;
+    }
+    __syncthreads();
+    for (int i = tid; i < a.n_split * G; i += DEC_THREADS) {
+        const int s = i / G, h = i % G;
+        const float Ms = (cM[h] == -INFINITY) ? 0.f : cM[h];
+        cw[i] = exp2_fast(base[(int64_t)s * rs + G * D + h] - Ms);
+    }
+    __syncthreads();
+    if (tid < G) {
+        float L = 0.f;
+        for (int s = 0; s < a.n_split; ++s) L = fmaf(cw[s * G + tid], base[(int64_t)s * rs + G * D + G + tid], L);
+        cL[tid] = L;
+    }
+    __syncthreads();
+    for (int o = tid; o < G * D; o += DEC_THREADS) {
+        const int h = o / D;
+        float s = 0.f;
+        for (int sp = 0; sp < a.n_split; ++sp) s = fmaf(cw[sp * G + h], base[(int64_t)sp * rs + o], s);
+        const float L = cL[h];
+        a.dst[((int64_t)b * a.hq + g * G + h) * D + (o % D)] = (L == 0.f) ? 0.f : s / L;
+    }
+    if (tid == 0) a.counters[pair] = 0u;
+}
+
+template <int D, int G>
+static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
+    dim3 grid(a.n_split, a.hkv, a.b);
+    hipLaunchKernelGGL((fa_decode_kernel<D, G>), grid, dim3(DEC_THREADS), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t st) {
+    if (a.n_split < 1 || a.n_split > DEC_MAX_SPLIT) return hipErrorInvalidValue;
+    if (head_dim == 128) {
+        if (group == 4) return launch_dg<128, 4>(a, st);
+        if (group == 2) return launch_dg<128, 2>(a, st);
+        if (group == 1) return launch_dg<128, 1>(a, st);
+    } else if (head_dim == 64) {
+        if (group == 4) return launch_dg<64, 4>(a, st);
+        if (group == 2) return launch_dg<64, 2>(a, st);
+        if (group == 1) return launch_dg<64, 1>(a, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+__global__ void zero_kernel(float* dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = 0.f;
+}
+
+hipError_t launch_zero(float* dst, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, n);
+    return hipGetLastError();
+}
+
+}  // namespace vxfa

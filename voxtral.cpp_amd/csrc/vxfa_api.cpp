@@ -1,0 +1,269 @@
+// vxfa_api.cpp — the C ABI of include/vxfa.h: contract validation (the
+// supports_op analogue), per-stream context with the split-KV workspace, and
+// dispatch to the gfx950 kernels.
+//
+// The validation rules restate the asserts ggml_flash_attn_ext makes when it
+// builds the node (q/k/v/mask shapes, GQA and batch broadcast divisibility)
+// and the CPU kernel's layout requirements (contiguous rows, dst contiguous
+// in the permuted order), as used at src/voxtral.cpp:1611 and :1802.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "../../include/vxfa.h"
+#include "fa_common.h"
+
+struct vxfa_ctx {
+    int device = 0;
+    float* ws = nullptr;
+    size_t ws_floats = 0;
+    uint32_t* counters = nullptr;
+    size_t n_counters = 0;
+    char last_error[256] = {0};
+};
+
+namespace {
+
+constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
+
+void set_err(vxfa_ctx* c, const char* fmt, ...) {
+    if (!c) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(c->last_error, sizeof(c->last_error), fmt, ap);
+    va_end(ap);
+}
+
+int elt_size(int32_t t) { return t == VXFA_TYPE_F32 ? 4 : (t == VXFA_TYPE_F16 ? 2 : 0); }
+
+bool aligned16(const void* p, size_t off) { return ((reinterpret_cast<uintptr_t>(p) + off) & 15u) == 0; }
+
+// Returns VXFA_OK / VXFA_INVALID_ARG / VXFA_UNSUPPORTED and a reason.
+int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
+          const vxfa_tensor* dst, float scale, float max_bias, float softcap, const char** why) {
+    *why = "";
+    if (!q || !k || !v || !dst) { *why = "q, k, v and dst are required"; return VXFA_INVALID_ARG; }
+    const vxfa_tensor* all[5] = {q, k, v, dst, mask};
+    for (int i = 0; i < 5; ++i) {
+        if (!all[i]) continue;
+        if (!elt_size(all[i]->type)) { *why = "unknown tensor type"; return VXFA_INVALID_ARG; }
+        for (int d = 0; d < 4; ++d)
+            if (all[i]->ne[d] < 0) { *why = "negative ne"; return VXFA_INVALID_ARG; }
+    }
+    // ggml_flash_attn_ext node construction rules
+    if (q->ne[0] != k->ne[0]) { *why = "q->ne[0] != k->ne[0]"; return VXFA_INVALID_ARG; }
+    if (k->ne[1] != v->ne[1]) { *why = "k->ne[1] != v->ne[1]"; return VXFA_INVALID_ARG; }
+    if (k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3]) { *why = "k/v head or batch mismatch"; return VXFA_INVALID_ARG; }
+    if (k->ne[2] == 0 || k->ne[3] == 0) { *why = "k has no heads or batches"; return VXFA_INVALID_ARG; }
+    if (q->ne[2] % k->ne[2]) { *why = "q heads not a multiple of kv heads"; return VXFA_INVALID_ARG; }
+    if (q->ne[3] % k->ne[3]) { *why = "q batch not a multiple of kv batch"; return VXFA_INVALID_ARG; }
+    if (mask) {
+        if (mask->ne[0] != k->ne[1]) { *why = "mask->ne[0] != n_kv"; return VXFA_INVALID_ARG; }
+        if (mask->ne[1] < q->ne[1]) { *why = "mask has fewer rows than q"; return VXFA_INVALID_ARG; }
+        if (mask->ne[2] == 0 || mask->ne[3] == 0) { *why = "mask has no planes"; return VXFA_INVALID_ARG; }
+        if (q->ne[2] % mask->ne[2] || q->ne[3] % mask->ne[3]) { *why = "mask does not broadcast over q"; return VXFA_INVALID_ARG; }
+        if (mask->nb[0] != (size_t)elt_size(mask->type)) { *why = "mask rows not contiguous"; return VXFA_INVALID_ARG; }
+    }
+    if (dst->ne[0] != v->ne[0] || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || dst->ne[3] != q->ne[3]) {
+        *why = "dst shape must be [Dv, Hq, Nq, B]";
+        return VXFA_INVALID_ARG;
+    }
+    if (q->nb[0] != (size_t)elt_size(q->type) || k->nb[0] != (size_t)elt_size(k->type) ||
+        v->nb[0] != (size_t)elt_size(v->type)) {
+        *why = "q/k/v rows must be contiguous";
+        return VXFA_INVALID_ARG;
+    }
+    // what this path implements
+    if (k->type != VXFA_TYPE_F16 || v->type != VXFA_TYPE_F16) { *why = "k and v must be F16"; return VXFA_UNSUPPORTED; }
+    if (mask && mask->type != VXFA_TYPE_F16) { *why = "mask must be F16"; return VXFA_UNSUPPORTED; }
+    if (dst->type != VXFA_TYPE_F32) { *why = "dst must be F32"; return VXFA_UNSUPPORTED; }
+    if (dst->nb[0] != 4 || dst->nb[1] != 4 * (size_t)dst->ne[0] || dst->nb[2] != dst->nb[1] * (size_t)dst->ne[1] ||
+        dst->nb[3] != dst->nb[2] * (size_t)dst->ne[2]) {
+        *why = "dst must be contiguous";
+        return VXFA_UNSUPPORTED;
+    }
+    if (k->ne[0] != v->ne[0]) { *why = "Dk != Dv"; return VXFA_UNSUPPORTED; }
+    if (k->ne[0] != 64 && k->ne[0] != 128) { *why = "head dim must be 64 or 128"; return VXFA_UNSUPPORTED; }
+    if (max_bias != 0.0f) { *why = "max_bias (ALiBi) not implemented"; return VXFA_UNSUPPORTED; }
+    if (softcap != 0.0f) { *why = "logit_softcap not implemented"; return VXFA_UNSUPPORTED; }
+    if (!isfinite(scale)) { *why = "scale must be finite"; return VXFA_UNSUPPORTED; }
+    const int64_t lim = 0x7fffffff;
+    if (q->ne[1] > lim || k->ne[1] > lim || q->ne[2] > 65535 || q->ne[3] > 65535) {
+        *why = "sizes beyond the launch limits";
+        return VXFA_UNSUPPORTED;
+    }
+    // 128-bit loads: q/k/v rows and dst rows must be 16-byte aligned
+    const vxfa_tensor* vec[4] = {q, k, v, dst};
+    for (int i = 0; i < 4; ++i) {
+        if (!aligned16(vec[i]->data, 0) || (vec[i]->nb[1] & 15) || (vec[i]->nb[2] & 15) || (vec[i]->nb[3] & 15)) {
+            *why = "q/k/v/dst data and strides must be 16-byte aligned";
+            return VXFA_UNSUPPORTED;
+        }
+    }
+    if (mask && ((reinterpret_cast<uintptr_t>(mask->data) & 1u) || (mask->nb[1] & 1) || (mask->nb[2] & 1) ||
+                 (mask->nb[3] & 1))) {
+        *why = "mask must be 2-byte aligned";
+        return VXFA_UNSUPPORTED;
+    }
+    return VXFA_OK;
+}
+
+// Workgroups per (batch, kv head) for the decode kernel: enough to cover the
+// chip twice over (256 CUs), at least 128 positions per workgroup, and at
+// most 64 so the final merge stays short.
+int choose_split(int64_t pairs, int64_t nkv) {
+    const int64_t target = 512;
+    int64_t s = (target + pairs - 1) / pairs;
+    const int64_t by_len = (nkv + 127) / 128;
+    if (s > by_len) s = by_len;
+    if (s > 64) s = 64;
+    if (s < 1) s = 1;
+    return (int)s;
+}
+
+}  // namespace
+
+extern "C" {
+
+vxfa_ctx* vxfa_ctx_create(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return nullptr;
+    vxfa_ctx* c = new (std::nothrow) vxfa_ctx();
+    if (!c) return nullptr;
+    c->device = device;
+    return c;
+}
+
+void vxfa_ctx_destroy(vxfa_ctx* c) {
+    if (!c) return;
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(c->device);
+    if (c->ws || c->counters) (void)hipDeviceSynchronize();
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->counters) (void)hipFree(c->counters);
+    (void)hipSetDevice(prev);
+    delete c;
+}
+
+int vxfa_supports(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
+                  const vxfa_tensor* dst, float scale, float max_bias, float logit_softcap) {
+    const char* why = nullptr;
+    return check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
+}
+
+const char* vxfa_status_str(int s) {
+    switch (s) {
+        case VXFA_OK: return "ok";
+        case VXFA_UNSUPPORTED: return "unsupported";
+        case VXFA_INVALID_ARG: return "invalid argument";
+        case VXFA_NO_WORKSPACE: return "no workspace";
+        case VXFA_HIP_ERROR: return "hip error";
+        default: return "unknown status";
+    }
+}
+
+const char* vxfa_last_error(const vxfa_ctx* c) { return c ? c->last_error : ""; }
+
+int vxfa_version(void) { return kVersion; }
+
+int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v,
+                        const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap,
+                        void* stream) {
+    if (!c) return VXFA_INVALID_ARG;
+    c->last_error[0] = 0;
+    const char* why = nullptr;
+    const int rc = check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
+    if (rc != VXFA_OK) {
+        set_err(c, "%s", why);
+        return rc;
+    }
+    const int64_t D = q->ne[0], Nq = q->ne[1], Hq = q->ne[2], B = q->ne[3];
+    const int64_t Nkv = k->ne[1], Hkv = k->ne[2];
+    if (Nq * Hq * B == 0) return VXFA_OK;
+
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) { set_err(c, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+
+    if (Nkv == 0) {
+        e = vxfa::launch_zero(static_cast<float*>(dst->data), Nq * Hq * B * D, st);
+        if (e != hipSuccess) { set_err(c, "zero fill: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+        return VXFA_OK;
+    }
+
+    vxfa::AttnArgs a;
+    memset(&a, 0, sizeof(a));
+    a.q = q->data;
+    a.k = static_cast<const _Float16*>(k->data);
+    a.v = static_cast<const _Float16*>(v->data);
+    a.mask = mask ? static_cast<const uint16_t*>(mask->data) : nullptr;
+    a.dst = static_cast<float*>(dst->data);
+    a.q_nb1 = (int64_t)q->nb[1]; a.q_nb2 = (int64_t)q->nb[2]; a.q_nb3 = (int64_t)q->nb[3];
+    a.k_nb1 = (int64_t)k->nb[1]; a.k_nb2 = (int64_t)k->nb[2]; a.k_nb3 = (int64_t)k->nb[3];
+    a.v_nb1 = (int64_t)v->nb[1]; a.v_nb2 = (int64_t)v->nb[2]; a.v_nb3 = (int64_t)v->nb[3];
+    if (mask) { a.m_nb1 = (int64_t)mask->nb[1]; a.m_nb2 = (int64_t)mask->nb[2]; a.m_nb3 = (int64_t)mask->nb[3]; }
+    a.nq = (int32_t)Nq; a.nkv = (int32_t)Nkv; a.hq = (int32_t)Hq; a.hkv = (int32_t)Hkv;
+    a.b = (int32_t)B; a.bk = (int32_t)k->ne[3];
+    a.hm = mask ? (int32_t)mask->ne[2] : 1;
+    a.bm = mask ? (int32_t)mask->ne[3] : 1;
+    a.q_f16 = q->type == VXFA_TYPE_F16;
+    a.scale_log2 = scale * vxfa::kLog2e;
+
+    const int64_t G = Hq / Hkv;
+    if (Nq == 1 && (G == 1 || G == 2 || G == 4)) {
+        const int S = choose_split(B * Hkv, Nkv);
+        a.n_split = S;
+        if (S > 1) {
+            const size_t need = (size_t)(B * Hkv) * S * G * (D + 2);
+            const size_t need_cnt = (size_t)(B * Hkv);
+            if (need > c->ws_floats || need_cnt > c->n_counters) {
+                // grow: wait for work that may still read the old buffers
+                if (c->ws || c->counters) (void)hipStreamSynchronize(st);
+                if (need > c->ws_floats) {
+                    if (c->ws) (void)hipFree(c->ws);
+                    c->ws = nullptr; c->ws_floats = 0;
+                    if (hipMalloc(&c->ws, need * sizeof(float)) != hipSuccess) {
+                        c->ws = nullptr;
+                        set_err(c, "workspace allocation of %zu bytes failed", need * sizeof(float));
+                        return VXFA_NO_WORKSPACE;
+                    }
+                    c->ws_floats = need;
+                }
+                if (need_cnt > c->n_counters) {
+                    if (c->counters) (void)hipFree(c->counters);
+                    c->counters = nullptr; c->n_counters = 0;
+                    if (hipMalloc(&c->counters, need_cnt * sizeof(uint32_t)) != hipSuccess) {
+                        c->counters = nullptr;
+                        set_err(c, "counter allocation failed");
+                        return VXFA_NO_WORKSPACE;
+                    }
+                    if (hipMemsetAsync(c->counters, 0, need_cnt * sizeof(uint32_t), st) != hipSuccess) {
+                        set_err(c, "counter clear failed");
+                        return VXFA_HIP_ERROR;
+                    }
+                    c->n_counters = need_cnt;
+                }
+            }
+            a.ws = c->ws;
+            a.counters = c->counters;
+        }
+        e = vxfa::launch_decode(a, (int)D, (int)G, st);
+    } else {
+        const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
+        const int waves = wg4 >= 256 ? 4 : 2;
+        e = vxfa::launch_prefill(a, (int)D, waves, st);
+    }
+    if (e != hipSuccess) {
+        set_err(c, "kernel launch: %s", hipGetErrorString(e));
+        return VXFA_HIP_ERROR;
+    }
+    return VXFA_OK;
+}
+
+}  // extern "C"
