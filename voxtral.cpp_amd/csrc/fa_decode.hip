@@ -53,7 +53,10 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
     __shared__ int lds_lo[DEC_WAVES], lds_hi[DEC_WAVES];
     __shared__ int lds_last;
     __shared__ float cw[DEC_MAX_SPLIT * G];
-    __shared__ float cM[G], cL[G];
+    __shared__ float cm[DEC_MAX_SPLIT * G];
+    __shared__ float cl[DEC_MAX_SPLIT * G];
+    __shared__ float cL[G];
+    __shared__ floatx4 cpart[DEC_THREADS / (G * D / 4)][G * D / 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -269,32 +272,61 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
     if (!lds_last) return;
     __threadfence();
 
+    // Every load below is independent of the others, so the whole merge costs
+    // about two round trips to L2 instead of one per split.
     const float* base = a.ws + (int64_t)pair * a.n_split * (G * (D + 2));
     const int rs = G * (D + 2);
+    const int nsg = a.n_split * G;
+    for (int i = tid; i < nsg; i += DEC_THREADS) {
+        const int s = i / G, h = i % G;
+        cm[i] = base[(int64_t)s * rs + G * D + h];
+        cl[i] = base[(int64_t)s * rs + G * D + G + h];
+    }
+    __syncthreads();
     if (tid < G) {
         float M = -INFINITY;
-        for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, base[(int64_t)s * rs + G * D + tid]);
-        cM[tid] = M;
-    }
-    __syncthreads();
-    for (int i = tid; i < a.n_split * G; i += DEC_THREADS) {
-        const int s = i / G, h = i % G;
-        const float Ms = (cM[h] == -INFINITY) ? 0.f : cM[h];
-        cw[i] = exp2_fast(base[(int64_t)s * rs + G * D + h] - Ms);
-    }
-    __syncthreads();
-    if (tid < G) {
+        for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, cm[s * G + tid]);
+        const float Ms = (M == -INFINITY) ? 0.f : M;
         float L = 0.f;
-        for (int s = 0; s < a.n_split; ++s) L = fmaf(cw[s * G + tid], base[(int64_t)s * rs + G * D + G + tid], L);
+        for (int s = 0; s < a.n_split; ++s) {
+            const float w = exp2_fast(cm[s * G + tid] - Ms);
+            cw[s * G + tid] = w;
+            L = fmaf(w, cl[s * G + tid], L);
+        }
         cL[tid] = L;
     }
     __syncthreads();
-    for (int o = tid; o < G * D; o += DEC_THREADS) {
-        const int h = o / D;
-        float s = 0.f;
-        for (int sp = 0; sp < a.n_split; ++sp) s = fmaf(cw[sp * G + h], base[(int64_t)sp * rs + o], s);
+    constexpr int NF = G * D / 4;                 // float4 outputs
+    constexpr int NPART = DEC_THREADS / NF;       // threads per output
+    static_assert(NPART >= 1 && NF * NPART == DEC_THREADS, "combine split");
+    {
+        const int f = tid % NF, part = tid / NF;
+        const int h = (4 * f) / D;
+        floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 16
+        for (int sp = part; sp < a.n_split; sp += NPART) {
+            const floatx4 x = *(const floatx4*)(base + (int64_t)sp * rs + 4 * f);
+            const float w = cw[sp * G + h];
+            acc4[0] = fmaf(w, x[0], acc4[0]);
+            acc4[1] = fmaf(w, x[1], acc4[1]);
+            acc4[2] = fmaf(w, x[2], acc4[2]);
+            acc4[3] = fmaf(w, x[3], acc4[3]);
+        }
+        cpart[part][f] = acc4;
+    }
+    __syncthreads();
+    if (tid < NF) {
+        floatx4 acc4 = cpart[0][tid];
+#pragma unroll
+        for (int p = 1; p < NPART; ++p) {
+            const floatx4 y = cpart[p][tid];
+            acc4[0] += y[0]; acc4[1] += y[1]; acc4[2] += y[2]; acc4[3] += y[3];
+        }
+        const int h = (4 * tid) / D, d = (4 * tid) % D;
         const float L = cL[h];
-        a.dst[((int64_t)b * a.hq + g * G + h) * D + (o % D)] = (L == 0.f) ? 0.f : s / L;
+        const float inv = (L == 0.f) ? 0.f : 1.0f / L;
+        floatx4 out = {acc4[0] * inv, acc4[1] * inv, acc4[2] * inv, acc4[3] * inv};
+        *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G + h) * D + d) = out;
     }
     if (tid == 0) a.counters[pair] = 0u;
 }

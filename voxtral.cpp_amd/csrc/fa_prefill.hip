@@ -21,10 +21,15 @@
 //   rescale runs on few tiles; P then stays below 256, safe in f16.
 // Row-to-KV mapping inside a 32-position block (lane half hh, element j of
 // the MFMA accumulator, a = j / 4, b = j % 4):
-//   hh = 0 : kv = 4a + b            hh = 1 : kv = 16 + 4(3 - a) + b
-// chosen so that the rows one 16-lane LDS phase reads fall in 16 distinct
-// bank groups with a 16-byte row padding.
+//   hh = 0 : kv = 4a + b            hh = 1 : kv = 16 + 4((a + 2) & 3) + b
+// chosen so that (1) the K rows one 16-lane LDS phase reads fall in 16
+// distinct bank groups with a 16-byte row padding, and (2) each half of a
+// lane's accumulator (j < 8, j >= 8) covers 8 contiguous positions in
+// increasing order, so P feeds the P.V MFMA without any register permutation
+// and V^T is fetched with one 128-bit read.
 #include "fa_common.h"
+
+#include <type_traits>
 
 namespace vxfa {
 
@@ -33,7 +38,7 @@ constexpr float PF_TAU = 8.0f;
 constexpr int PF_MAX_TILE_WORDS = 256;   // live-tile bitmap: up to 8192 tiles
 
 __device__ __forceinline__ int pf_kv_of(int hh, int j) {
-    return hh ? 16 + 4 * (3 - (j >> 2)) + (j & 3) : j;
+    return hh ? 16 + (((j >> 2) + 2) & 3) * 4 + (j & 3) : j;
 }
 
 template <int D, int NW, bool MASK>
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(64 * NW) void fa_prefill_kernel(AttnArgs a) {
     int krow[2];
     {
         const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
-        const int kv = ahb ? 16 + 4 * (3 - am) + ab : 4 * am + ab;
+        const int kv = ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
         krow[0] = kv;
         krow[1] = 32 + kv;
     }
@@ -177,17 +182,12 @@ __global__ __launch_bounds__(64 * NW) void fa_prefill_kernel(AttnArgs a) {
     if (MASK) mrow = (const uint16_t*)((const char*)mplane + (int64_t)(qvalid ? qrow : 0) * a.m_nb1);
     const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    int t = next_tile(0);
-    if (t < ntile) gload(t);
-    int buf = 0;
-    while (t < ntile) {
-        swrite(buf);
-        __syncthreads();
-        const int tn = next_tile(t + 1);
-        if (tn < ntile) gload(tn);
+    const float c = a.scale_log2;
 
-        const int kv0 = t * PF_BN;
-        const bool tail = kv0 + PF_BN > a.nkv;
+    // One KV tile for this wavefront. TAIL: the tile runs past n_kv, so
+    // positions >= n_kv are forced to -inf (only the last tile can be).
+    auto tile_body = [&](auto tail_tag, int buf, int kv0) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
 
         // mask values for this lane's 32 scores
         float mv[2][16];
@@ -220,19 +220,37 @@ __global__ __launch_bounds__(64 * NW) void fa_prefill_kernel(AttnArgs a) {
                 }
             }
 
-            float mx = -INFINITY;
+            // Row max in log2 units. Without a mask the scale is applied after
+            // the max (max(c*s) = c*max(s) for c >= 0, c*min(s) for c < 0) and
+            // folded into the exp2 argument below, one FMA per score.
+            float mx;
+            if (MASK || TAIL) {
+                mx = -INFINITY;
 #pragma unroll
-            for (int kvb = 0; kvb < 2; ++kvb)
+                for (int kvb = 0; kvb < 2; ++kvb)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    float x = st[kvb][j] * a.scale_log2;
-                    if (MASK) x += mv[kvb][j];
-                    if (!MASK && tail) {
-                        if (kv0 + 32 * kvb + pf_kv_of(hh, j) >= a.nkv) x = -INFINITY;
+                    for (int j = 0; j < 16; ++j) {
+                        float x = st[kvb][j] * c;
+                        if (MASK) x = (mv[kvb][j] == -INFINITY) ? -INFINITY : x + mv[kvb][j];
+                        if (TAIL && kv0 + 32 * kvb + pf_kv_of(hh, j) >= a.nkv) x = -INFINITY;
+                        st[kvb][j] = x;
+                        mx = fmaxf(mx, x);
                     }
-                    st[kvb][j] = x;
-                    mx = fmaxf(mx, x);
-                }
+            } else if (c >= 0.f) {
+                float r = st[0][0];
+#pragma unroll
+                for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) r = fmaxf(r, st[kvb][j]);
+                mx = r * c;
+            } else {
+                float r = st[0][0];
+#pragma unroll
+                for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) r = fminf(r, st[kvb][j]);
+                mx = r * c;
+            }
             mx = fmaxf(mx, shfl_xor(mx, 32));
 
             if (__any(mx > m_run + PF_TAU)) {
@@ -254,15 +272,16 @@ __global__ __launch_bounds__(64 * NW) void fa_prefill_kernel(AttnArgs a) {
                 half8 pb;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const int j = hh ? 8 * cc + ((i + 4) & 7) : 8 * cc + i;
-                    pb[i] = (_Float16)exp2_fast(st[kvb][j] - msafe);
+                    const float e = (MASK || TAIL) ? st[kvb][8 * cc + i] - msafe
+                                                   : fmaf(st[kvb][8 * cc + i], c, -msafe);
+                    pb[i] = (_Float16)exp2_fast(e);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     half2 p2 = {pb[2 * i], pb[2 * i + 1]};
                     l_run = __builtin_amdgcn_fdot2(p2, ones, l_run, false);
                 }
-                const int kvl = 32 * kvb + (hh ? 16 + 8 * (1 - cc) : 8 * cc);
+                const int kvl = 32 * kvb + (hh ? 16 + 8 * (1 - cc) : 8 * cc);  // 8 positions, increasing
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
                     const half8 va = *(const half8*)&sVT[buf][(32 * db + nl) * VSTR + kvl];
@@ -270,6 +289,19 @@ __global__ __launch_bounds__(64 * NW) void fa_prefill_kernel(AttnArgs a) {
                 }
             }
         }
+    };
+
+    int t = next_tile(0);
+    if (t < ntile) gload(t);
+    int buf = 0;
+    while (t < ntile) {
+        swrite(buf);
+        __syncthreads();
+        const int tn = next_tile(t + 1);
+        if (tn < ntile) gload(tn);
+        const int kv0 = t * PF_BN;
+        if (kv0 + PF_BN > a.nkv) tile_body(std::true_type{}, buf, kv0);
+        else tile_body(std::false_type{}, buf, kv0);
         buf ^= 1;
         t = tn;
     }

@@ -11,6 +11,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <new>
@@ -25,6 +26,10 @@ struct vxfa_ctx {
     uint32_t* counters = nullptr;
     size_t n_counters = 0;
     char last_error[256] = {0};
+    // launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
+    // VXFA_PREFILL_WAVES), read once when the context is created; 0 = heuristic
+    int split_override = 0;
+    int waves_override = 0;
 };
 
 namespace {
@@ -136,6 +141,8 @@ vxfa_ctx* vxfa_ctx_create(int device) {
     vxfa_ctx* c = new (std::nothrow) vxfa_ctx();
     if (!c) return nullptr;
     c->device = device;
+    if (const char* e = getenv("VXFA_DECODE_SPLIT")) c->split_override = atoi(e);
+    if (const char* e = getenv("VXFA_PREFILL_WAVES")) c->waves_override = atoi(e);
     return c;
 }
 
@@ -217,7 +224,8 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
 
     const int64_t G = Hq / Hkv;
     if (Nq == 1 && (G == 1 || G == 2 || G == 4)) {
-        const int S = choose_split(B * Hkv, Nkv);
+        int S = choose_split(B * Hkv, Nkv);
+        if (c->split_override > 0) S = c->split_override < 64 ? c->split_override : 64;
         a.n_split = S;
         if (S > 1) {
             const size_t need = (size_t)(B * Hkv) * S * G * (D + 2);
@@ -256,7 +264,8 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
         const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
-        const int waves = wg4 >= 256 ? 4 : 2;
+        int waves = wg4 >= 256 ? 4 : 2;
+        if (c->waves_override == 2 || c->waves_override == 4) waves = c->waves_override;
         e = vxfa::launch_prefill(a, (int)D, waves, st);
     }
     if (e != hipSuccess) {
