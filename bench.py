@@ -142,24 +142,44 @@ def prefill_layers(torch, n_layers, n=439, hq=32, hkv=8, hd=128, seed=3000):
 # ---------------------------------------------------------------------------
 # timing
 
-def time_calls(torch, ctx, calls, steps, warmup):
-    """calls: list of Layer for one step. Returns (ms per step, µs per call)."""
-    stream = torch.cuda.current_stream()
-    sh = stream.cuda_stream
+def time_calls(torch, ctx, calls, steps, warmup, graph=True):
+    """Time `steps` passes over `calls` (one step = every call once).
 
-    def one_step():
+    The step is captured once into a HIP graph (torch.cuda.CUDAGraph records
+    the library's launches on the capture stream) and replayed, so the timed
+    region measures the kernels rather than the Python ctypes call per layer.
+    Events are recorded on the stream the kernels run on. Returns
+    (ms per step, µs per call)."""
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def one_step(sh):
         for L in calls:
             ctx.flash_attn_ext(L.q, L.k, L.v, L.mask, L.dst, L.scale, stream=sh)
 
-    for _ in range(warmup):
-        one_step()
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, warmup)):   # also sizes the workspace before capture
+            one_step(stream.cuda_stream)
     torch.cuda.synchronize()
+    g = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            one_step(stream.cuda_stream)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        one_step()
-    end.record(stream)
+    with torch.cuda.stream(stream):   # replay() launches on the current stream
+        start.record(stream)
+        for _ in range(steps):
+            if g is not None:
+                g.replay()
+            else:
+                one_step(stream.cuda_stream)
+        end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
     return ms / steps, 1000.0 * ms / (steps * len(calls))

@@ -215,3 +215,46 @@ def test_unsupported_types_are_reported(runner):
     c.views["k"] = ("k32", oracle.F32, ne, tuple(x * 2 for x in nb), 0)
     rc, _ = runner.run(c, check=False)
     assert rc == gpu_util.vxfa.UNSUPPORTED
+
+
+def test_graph_capture_replays_match_eager(runner):
+    """Calls captured into a HIP graph (decode split+merge, masked prefill)
+    replay to the same bits as eager calls, with eager work between replays."""
+    import torch
+    import gpu_util
+    cs = [cases.decode_case(8192, seed=41), cases.prefill_case(100, hq=8, hkv=2, seed=42)]
+    devs = [gpu_util.to_device(c) for c in cs]
+    outs = []
+    eager = []
+    for c, d in zip(cs, devs):
+        _, ref = runner.run(c, dev=d)
+        eager.append(ref)
+        B, Nq, Hq, D = c.out_shape
+        outs.append(torch.zeros(B * Nq * Hq * D, device="cuda", dtype=torch.float32))
+    stream = torch.cuda.Stream()
+    descs = [gpu_util.descs(c, d) for c, d in zip(cs, devs)]
+
+    def step():
+        for c, dd, o in zip(cs, descs, outs):
+            ne, nb = c.dst_ne_nb()
+            dst = gpu_util.vxfa.desc(o.data_ptr(), gpu_util.vxfa.F32, ne, nb)
+            runner.ctx.flash_attn_ext(dd["q"], dd["k"], dd["v"], dd.get("mask"), dst, c.scale,
+                                      stream=stream.cuda_stream)
+
+    with torch.cuda.stream(stream):
+        step()  # sizes the workspace outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        runner.run(cs[0], dev=devs[0])  # eager work between replays
+        for o, ref, c in zip(outs, eager, cs):
+            got = o.cpu().numpy().reshape(c.out_shape)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (rep, c.name)

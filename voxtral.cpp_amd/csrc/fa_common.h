@@ -26,7 +26,6 @@ struct AttnArgs {
     const uint16_t* mask; // F16 bits, may be null
     float* dst;           // [B][Nq][Hq][D]
     float* ws;            // split-KV partials (decode)
-    uint32_t* counters;   // split-KV arrival counters (decode), self-resetting
     int64_t q_nb1, q_nb2, q_nb3;   // bytes
     int64_t k_nb1, k_nb2, k_nb3;   // bytes
     int64_t v_nb1, v_nb2, v_nb3;   // bytes
@@ -61,19 +60,29 @@ __device__ __forceinline__ half8 load_q8(const void* base, int64_t byte_off, boo
 // Cross-lane helpers over a 64-lane wavefront.
 __device__ __forceinline__ float shfl_xor(float x, int m) { return __shfl_xor(x, m, 64); }
 
-// max / sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15)
+// DPP row rotate: lane i of each 16-lane row reads lane (i + n) mod 16 of the
+// same row (dpp_ctrl ROW_ROR = 0x120 + n). A VALU operand modifier, no LDS.
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+    static_assert(N >= 1 && N <= 15, "rotate amount");
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF,
+                                                                 false));
+}
+
+// max / sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane
+// of the row receives the result
 __device__ __forceinline__ float row16_max(float x) {
-    x = fmaxf(x, shfl_xor(x, 8));
-    x = fmaxf(x, shfl_xor(x, 4));
-    x = fmaxf(x, shfl_xor(x, 2));
-    x = fmaxf(x, shfl_xor(x, 1));
+    x = fmaxf(x, row_ror<8>(x));
+    x = fmaxf(x, row_ror<4>(x));
+    x = fmaxf(x, row_ror<2>(x));
+    x = fmaxf(x, row_ror<1>(x));
     return x;
 }
 __device__ __forceinline__ float row16_sum(float x) {
-    x += shfl_xor(x, 8);
-    x += shfl_xor(x, 4);
-    x += shfl_xor(x, 2);
-    x += shfl_xor(x, 1);
+    x += row_ror<8>(x);
+    x += row_ror<4>(x);
+    x += row_ror<2>(x);
+    x += row_ror<1>(x);
     return x;
 }
 
@@ -82,6 +91,7 @@ __device__ __forceinline__ float row16_sum(float x) {
 // Host-side launchers (implemented in the kernel translation units).
 namespace vxfa {
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t stream);
+constexpr int kDecodeMaxSplit = 64;
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 }  // namespace vxfa

@@ -6,28 +6,34 @@
 // n_tokens = 1 (step graphs :1959-1962 and :2050-2053), where every KV head
 // serves G = Hq / Hkv query heads (32 / 8 = 4).
 //
-// Work decomposition
-//   grid  = (n_split, Hkv, B): one workgroup per (split of the live KV range,
-//           kv head, batch row); 4 wavefronts per workgroup.
-//   Each wavefront walks 32-position tiles of its workgroup's range.
-//   QK^T  : one v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims). The A
-//           operand holds the G query heads replicated 16/G times, so every
-//           lane receives the scores of all G heads for one position and no
-//           cross-lane reduction is needed for the dot products.
-//   K     : loaded straight from HBM into the MFMA B-operand layout
-//           (16 positions x 64 contiguous bytes per instruction, 128-bit).
-//   V     : loaded with 16 (hd128) or 8 (hd64) lanes per 256/128-byte row,
-//           fully coalesced 128-bit loads; P.V on the VALU with fp32
-//           accumulators (each lane owns 8 dims of all G heads).
-//   Softmax: fp32, exp2 with scale*log2(e) folded in, running max per head
-//           shared by the wavefront.
-//   Combine: wavefronts merge through LDS; with n_split > 1 each workgroup
-//           writes (O, m, l) for its split and the last workgroup to arrive
-//           (atomic counter, reset by that workgroup) merges all splits in a
-//           fixed order, so the output does not depend on arrival order.
+// Two kernels on the caller's stream:
+//   fa_decode_split   grid (n_split, Hkv, B), 4 wavefronts per workgroup.
+//                     Each workgroup reduces one contiguous slice of the live
+//                     KV range to (O, m, l) per query head of its group.
+//   fa_decode_combine grid (Hkv, B): log-sum-exp merge of the n_split
+//                     partials in a fixed order (deterministic output).
+// With n_split == 1 the split kernel writes the output and no merge runs.
+// The kernel boundary orders the partials' stores before the merge's loads;
+// an in-kernel last-block merge needs an agent-scope release fence (an L2
+// write-back per workgroup), which measured slower than the second launch.
+//
+// Inside a wavefront (32-position tiles, software pipelined: the next tile's
+// K/V loads are in flight while the current tile is computed):
+//   QK^T  v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims). The A operand
+//         holds the G query heads replicated 16/G times, so every lane gets
+//         the scores of all G heads for one position: no cross-lane dot
+//         reduction.
+//   K     loaded from HBM straight into the MFMA B-operand layout
+//         (16 positions x 64 contiguous bytes per 128-bit load instruction).
+//   V     16 (hd128) or 8 (hd64) lanes per row, fully coalesced 128-bit
+//         loads; P.V on the VALU with fp32 accumulators (each lane owns 8
+//         dims of all G heads); P is handed from the MFMA layout to the V
+//         layout through a 512-byte LDS slot per wavefront.
+//   Softmax fp32, exp2 with scale*log2(e) folded in, one running max per head
+//         shared by the wavefront (DPP row reductions).
 // Masks: an additive F16 mask is honoured exactly (-inf removes a position).
-// The workgroup first scans the mask row to find the live range, so a
-// sliding window or a ragged length only costs the live positions.
+// The workgroup first scans the mask row(s) for the live range, so a sliding
+// window or a ragged stream length only costs its live positions.
 #include "fa_common.h"
 
 namespace vxfa {
@@ -35,10 +41,9 @@ namespace vxfa {
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 constexpr int DEC_TILE = 32;
-constexpr int DEC_MAX_SPLIT = 64;
 
-template <int D, int G>
-__global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
+template <int D, int G, bool QF16, bool MASK>
+__global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     static_assert(D == 64 || D == 128, "head dim");
     static_assert(G == 1 || G == 2 || G == 4, "GQA group");
     constexpr int KS = D / 32;        // MFMA k-steps of 32 dims
@@ -51,12 +56,6 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
     __shared__ float lds_m[DEC_WAVES][G];
     __shared__ float lds_l[DEC_WAVES][G];
     __shared__ int lds_lo[DEC_WAVES], lds_hi[DEC_WAVES];
-    __shared__ int lds_last;
-    __shared__ float cw[DEC_MAX_SPLIT * G];
-    __shared__ float cm[DEC_MAX_SPLIT * G];
-    __shared__ float cl[DEC_MAX_SPLIT * G];
-    __shared__ float cL[G];
-    __shared__ floatx4 cpart[DEC_THREADS / (G * D / 4)][G * D / 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -65,16 +64,16 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
     const int g = blockIdx.y;
     const int b = blockIdx.z;
     const int bkv = b / (a.b / a.bk);
+    constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
 
     // ---- live range of the KV axis -------------------------------------
     int lo = 0, hi = a.nkv;
-    if (a.mask) {
+    if constexpr (masked) {
         int tlo = 0x7fffffff, thi = -1;
         const int nplanes = (a.hm == 1) ? 1 : G;
         for (int j = 0; j < nplanes; ++j) {
             const int hq = g * G + j;
-            const uint16_t* mrow = (const uint16_t*)((const char*)a.mask +
-                                                     (int64_t)(hq % a.hm) * a.m_nb2 +
+            const uint16_t* mrow = (const uint16_t*)((const char*)a.mask + (int64_t)(hq % a.hm) * a.m_nb2 +
                                                      (int64_t)(b % a.bm) * a.m_nb3);
             for (int i = tid; i < a.nkv; i += DEC_THREADS) {
                 if (mrow[i] != kF16NegInf) {
@@ -99,26 +98,75 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
     const int t_begin = (int)(((int64_t)ntiles * split) / a.n_split);
     const int t_end = (int)(((int64_t)ntiles * (split + 1)) / a.n_split);
 
-    // ---- Q operand: A[m][k], m = lane & 15 -> head (m % G), k-chunk lane >> 4
-    const int qelt = a.q_f16 ? 2 : 4;
-    half8 qa[KS];
-    {
-        const int hq = g * G + ((lane & 15) % G);
-        const int64_t qoff = (int64_t)hq * a.q_nb2 + (int64_t)b * a.q_nb3;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            qa[ks] = load_q8(a.q, qoff + (int64_t)(32 * ks + 8 * (lane >> 4)) * qelt, a.q_f16 != 0);
-    }
-
     const char* kb = (const char*)a.k + (int64_t)g * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)g * a.v_nb2 + (int64_t)bkv * a.v_nb3;
     const uint16_t* mplane[4] = {nullptr, nullptr, nullptr, nullptr};
-    if (a.mask) {
+    if constexpr (masked) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hq = g * G + (i % G);
             mplane[i] = (const uint16_t*)((const char*)a.mask + (int64_t)(hq % a.hm) * a.m_nb2 +
                                           (int64_t)(b % a.bm) * a.m_nb3);
+        }
+    }
+
+    const int kcol = 8 * (lane >> 4);     // dims owned in the K operand
+    const int vrow = lane / CH;           // row offset owned in the V layout
+    const int vcol = (lane % CH) * 8;     // dims owned in the V layout
+
+    struct Tile {
+        half8 k[2][KS];
+        half8 v[NV];
+        uint16_t m[2][4];
+    };
+    auto load_tile = [&](Tile& T, int t) {
+        const int p0 = lo + t * DEC_TILE;
+        const int pend = min(p0 + DEC_TILE, hi);
+#pragma unroll
+        for (int grp = 0; grp < 2; ++grp) {
+            const int pos = min(p0 + 16 * grp + (lane & 15), pend - 1);
+            const char* kp = kb + (int64_t)pos * a.k_nb1 + kcol * 2;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
+            if constexpr (masked) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) T.m[grp][i] = mplane[i][pos];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int pos = min(p0 + vrow + i * RPI, pend - 1);
+            T.v[i] = *(const half8*)(vb + (int64_t)pos * a.v_nb1 + vcol * 2);
+        }
+    };
+
+    // ---- prologue: Q and the first tile go out together -------------------
+    // (the Q element type is a template parameter: a load-or-convert branch on
+    // it makes the compiler wait for all global loads inside the KV loop)
+    const int hq_lane = g * G + ((lane & 15) % G);  // A-operand row m = lane & 15 -> head m % G
+    const int64_t qoff = (int64_t)hq_lane * a.q_nb2 + (int64_t)b * a.q_nb3;
+    constexpr int QCH = QF16 ? 1 : 2;                // 16-byte loads per 8 elements
+    floatx4 qraw[KS][QCH];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const floatx4* p = (const floatx4*)((const char*)a.q + qoff + (int64_t)(32 * ks + 8 * (lane >> 4)) * (QF16 ? 2 : 4));
+#pragma unroll
+        for (int u = 0; u < QCH; ++u) qraw[ks][u] = p[u];
+    }
+    Tile TA, TB;
+    int t = t_begin + wave;
+    if (t < t_end) load_tile(TA, t);
+    half8 qa[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        if constexpr (QF16) {
+            qa[ks] = __builtin_bit_cast(half8, qraw[ks][0]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qa[ks][e] = (_Float16)qraw[ks][0][e];
+                qa[ks][4 + e] = (_Float16)qraw[ks][QCH - 1][e];
+            }
         }
     }
 
@@ -131,52 +179,32 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
 
-    const int kcol = 8 * (lane >> 4);     // dims owned in the K operand
-    const int vrow = lane / CH;           // row offset owned in the V layout
-    const int vcol = (lane % CH) * 8;     // dims owned in the V layout
-
-    for (int t = t_begin + wave; t < t_end; t += DEC_WAVES) {
-        const int p0 = lo + t * DEC_TILE;
+    auto process = [&](const Tile& T, int tt) {
+        const int p0 = lo + tt * DEC_TILE;
         const int pend = min(p0 + DEC_TILE, hi);
-
-        half8 kr[2][KS];
-#pragma unroll
-        for (int grp = 0; grp < 2; ++grp) {
-            const int pos = min(p0 + 16 * grp + (lane & 15), pend - 1);
-            const char* kp = kb + (int64_t)pos * a.k_nb1 + kcol * 2;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[grp][ks] = *(const half8*)(kp + 64 * ks);
-        }
-        half8 vr[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int pos = min(p0 + vrow + i * RPI, pend - 1);
-            vr[i] = *(const half8*)(vb + (int64_t)pos * a.v_nb1 + vcol * 2);
-        }
-
         floatx4 sc[2];
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
             sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kr[grp][ks], sc[grp], 0, 0, 0);
+                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], T.k[grp][ks], sc[grp], 0, 0, 0);
         }
-
-        // scores in log2 units; lane holds heads i (= row 4*(lane>>4)+i mod G) at its position
+        // scores in log2 units; lane holds head (i % G) at position p0 + 16*grp + (lane & 15)
         float x[2][4];
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
-            const int pos = p0 + 16 * grp + (lane & 15);
-            const bool valid = pos < pend;
+            const bool valid = p0 + 16 * grp + (lane & 15) < pend;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float mv = 0.f;
-                if (a.mask && valid) mv = f16_bits_to_f32(mplane[i][pos]) * kLog2e;
-                x[grp][i] = valid ? fmaf(sc[grp][i], a.scale_log2, mv) : -INFINITY;
+                float xv = sc[grp][i] * a.scale_log2;
+                if constexpr (masked) {
+                    const uint16_t mb = T.m[grp][i];
+                    xv = (mb == kF16NegInf) ? -INFINITY : fmaf(f16_bits_to_f32(mb), kLog2e, xv);
+                }
+                x[grp][i] = valid ? xv : -INFINITY;
             }
         }
-
         float alpha[4], p[2][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -189,27 +217,37 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
             l_run[i] = fmaf(l_run[i], alpha[i], p[0][i] + p[1][i]);
             m_run[i] = mnew;
         }
-
         if ((lane >> 4) == 0) {
             lds_p[wave][lane] = floatx4{p[0][0], p[0][1], p[0][2], p[0][3]};
             lds_p[wave][16 + lane] = floatx4{p[1][0], p[1][1], p[1][2], p[1][3]};
         }
         __builtin_amdgcn_wave_barrier();
-
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[h][j] *= alpha[h];
-
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const floatx4 pv = lds_p[wave][vrow + i * RPI];
 #pragma unroll
             for (int h = 0; h < G; ++h)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pv[h], (float)vr[i][j], acc[h][j]);
+                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pv[h], (float)T.v[i][j], acc[h][j]);
         }
         __builtin_amdgcn_wave_barrier();
+    };
+
+    // ---- main loop: two register sets, the next tile loads during compute ----
+    while (t < t_end) {
+        int tn = t + DEC_WAVES;
+        if (tn < t_end) load_tile(TB, tn);
+        process(TA, t);
+        t = tn;
+        if (t >= t_end) break;
+        tn = t + DEC_WAVES;
+        if (tn < t_end) load_tile(TA, tn);
+        process(TB, t);
+        t = tn;
     }
 
     // ---- merge lanes, then wavefronts ------------------------------------
@@ -237,8 +275,9 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    const int pair = b * a.hkv + g;
-    float* rec = a.ws + ((int64_t)pair * a.n_split + split) * (G * (D + 2));
+    float* rec = nullptr;
+    if (a.n_split > 1)
+        rec = a.ws + ((int64_t)(b * a.hkv + g) * a.n_split + split) * (G * (D + 2));
     for (int o = tid; o < G * D; o += DEC_THREADS) {
         const int h = o / D, d = o % D;
         float M = lds_m[0][h];
@@ -252,30 +291,34 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
             s = fmaf(wt, lds_acc[w][h][d], s);
             L = fmaf(wt, lds_l[w][h], L);
         }
-        if (a.n_split == 1) {
+        if (rec == nullptr) {
             a.dst[((int64_t)b * a.hq + g * G + h) * D + d] = (L == 0.f) ? 0.f : s / L;
         } else {
             rec[o] = s;
             if (d == 0) { rec[G * D + h] = M; rec[G * D + G + h] = L; }
         }
     }
-    if (a.n_split == 1) return;
+}
 
-    // ---- split combine by the last workgroup of this (batch, kv head) ----
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.counters[pair], 1u);
-        lds_last = (prev == (unsigned)(a.n_split - 1));
-    }
-    __syncthreads();
-    if (!lds_last) return;
-    __threadfence();
+// Log-sum-exp merge of the n_split partial records of one (kv head, batch):
+//   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
+// All loads are independent, so the merge costs about two round trips.
+template <int D, int G>
+__global__ __launch_bounds__(DEC_THREADS) void fa_decode_combine(AttnArgs a) {
+    constexpr int NF = G * D / 4;                 // float4 outputs
+    constexpr int NPART = DEC_THREADS / NF;       // threads per output
+    static_assert(NPART >= 1 && NF * NPART == DEC_THREADS, "combine split");
+    __shared__ float cw[kDecodeMaxSplit * G];
+    __shared__ float cm[kDecodeMaxSplit * G];
+    __shared__ float cl[kDecodeMaxSplit * G];
+    __shared__ float cL[G];
+    __shared__ floatx4 cpart[NPART][NF];
 
-    // Every load below is independent of the others, so the whole merge costs
-    // about two round trips to L2 instead of one per split.
-    const float* base = a.ws + (int64_t)pair * a.n_split * (G * (D + 2));
+    const int tid = threadIdx.x;
+    const int g = blockIdx.x;
+    const int b = blockIdx.y;
     const int rs = G * (D + 2);
+    const float* base = a.ws + (int64_t)(b * a.hkv + g) * a.n_split * rs;
     const int nsg = a.n_split * G;
     for (int i = tid; i < nsg; i += DEC_THREADS) {
         const int s = i / G, h = i % G;
@@ -296,9 +339,6 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
         cL[tid] = L;
     }
     __syncthreads();
-    constexpr int NF = G * D / 4;                 // float4 outputs
-    constexpr int NPART = DEC_THREADS / NF;       // threads per output
-    static_assert(NPART >= 1 && NF * NPART == DEC_THREADS, "combine split");
     {
         const int f = tid % NF, part = tid / NF;
         const int h = (4 * f) / D;
@@ -328,18 +368,26 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_kernel(AttnArgs a) {
         floatx4 out = {acc4[0] * inv, acc4[1] * inv, acc4[2] * inv, acc4[3] * inv};
         *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G + h) * D + d) = out;
     }
-    if (tid == 0) a.counters[pair] = 0u;
 }
 
 template <int D, int G>
 static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
-    dim3 grid(a.n_split, a.hkv, a.b);
-    hipLaunchKernelGGL((fa_decode_kernel<D, G>), grid, dim3(DEC_THREADS), 0, st, a);
+    const dim3 grid(a.n_split, a.hkv, a.b), block(DEC_THREADS);
+    if (a.mask) {
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode_split<D, G, true, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((fa_decode_split<D, G, false, true>), grid, block, 0, st, a);
+    } else {
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode_split<D, G, true, false>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((fa_decode_split<D, G, false, false>), grid, block, 0, st, a);
+    }
+    if (a.n_split > 1)
+        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv, a.b), dim3(DEC_THREADS), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t st) {
-    if (a.n_split < 1 || a.n_split > DEC_MAX_SPLIT) return hipErrorInvalidValue;
+    if (a.n_split < 1 || a.n_split > kDecodeMaxSplit) return hipErrorInvalidValue;
+    if (a.n_split > 1 && a.ws == nullptr) return hipErrorInvalidValue;
     if (head_dim == 128) {
         if (group == 4) return launch_dg<128, 4>(a, st);
         if (group == 2) return launch_dg<128, 2>(a, st);

@@ -23,8 +23,6 @@ struct vxfa_ctx {
     int device = 0;
     float* ws = nullptr;
     size_t ws_floats = 0;
-    uint32_t* counters = nullptr;
-    size_t n_counters = 0;
     char last_error[256] = {0};
     // launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
     // VXFA_PREFILL_WAVES), read once when the context is created; 0 = heuristic
@@ -118,9 +116,9 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
     return VXFA_OK;
 }
 
-// Workgroups per (batch, kv head) for the decode kernel: enough to cover the
-// chip twice over (256 CUs), at least 128 positions per workgroup, and at
-// most 64 so the final merge stays short.
+// Workgroups per (batch, kv head) for the decode split kernel: enough to
+// cover the chip twice over (256 CUs), at least 128 positions per workgroup,
+// and at most kDecodeMaxSplit so the merge stays short.
 int choose_split(int64_t pairs, int64_t nkv) {
     const int64_t target = 512;
     int64_t s = (target + pairs - 1) / pairs;
@@ -151,9 +149,10 @@ void vxfa_ctx_destroy(vxfa_ctx* c) {
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(c->device);
-    if (c->ws || c->counters) (void)hipDeviceSynchronize();
-    if (c->ws) (void)hipFree(c->ws);
-    if (c->counters) (void)hipFree(c->counters);
+    if (c->ws) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(c->ws);
+    }
     (void)hipSetDevice(prev);
     delete c;
 }
@@ -225,46 +224,34 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
     const int64_t G = Hq / Hkv;
     if (Nq == 1 && (G == 1 || G == 2 || G == 4)) {
         int S = choose_split(B * Hkv, Nkv);
-        if (c->split_override > 0) S = c->split_override < 64 ? c->split_override : 64;
+        if (c->split_override > 0) S = c->split_override < vxfa::kDecodeMaxSplit ? c->split_override : vxfa::kDecodeMaxSplit;
         a.n_split = S;
         if (S > 1) {
             const size_t need = (size_t)(B * Hkv) * S * G * (D + 2);
-            const size_t need_cnt = (size_t)(B * Hkv);
-            if (need > c->ws_floats || need_cnt > c->n_counters) {
-                // grow: wait for work that may still read the old buffers
-                if (c->ws || c->counters) (void)hipStreamSynchronize(st);
-                if (need > c->ws_floats) {
-                    if (c->ws) (void)hipFree(c->ws);
-                    c->ws = nullptr; c->ws_floats = 0;
-                    if (hipMalloc(&c->ws, need * sizeof(float)) != hipSuccess) {
-                        c->ws = nullptr;
-                        set_err(c, "workspace allocation of %zu bytes failed", need * sizeof(float));
-                        return VXFA_NO_WORKSPACE;
-                    }
-                    c->ws_floats = need;
+            if (need > c->ws_floats) {
+                // grow: work queued earlier on this stream may still read the old buffer
+                if (c->ws) {
+                    (void)hipStreamSynchronize(st);
+                    (void)hipFree(c->ws);
                 }
-                if (need_cnt > c->n_counters) {
-                    if (c->counters) (void)hipFree(c->counters);
-                    c->counters = nullptr; c->n_counters = 0;
-                    if (hipMalloc(&c->counters, need_cnt * sizeof(uint32_t)) != hipSuccess) {
-                        c->counters = nullptr;
-                        set_err(c, "counter allocation failed");
-                        return VXFA_NO_WORKSPACE;
-                    }
-                    if (hipMemsetAsync(c->counters, 0, need_cnt * sizeof(uint32_t), st) != hipSuccess) {
-                        set_err(c, "counter clear failed");
-                        return VXFA_HIP_ERROR;
-                    }
-                    c->n_counters = need_cnt;
+                c->ws = nullptr;
+                c->ws_floats = 0;
+                if (hipMalloc(&c->ws, need * sizeof(float)) != hipSuccess) {
+                    c->ws = nullptr;
+                    set_err(c, "workspace allocation of %zu bytes failed", need * sizeof(float));
+                    return VXFA_NO_WORKSPACE;
                 }
+                c->ws_floats = need;
             }
             a.ws = c->ws;
-            a.counters = c->counters;
         }
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
+        // query-row wavefronts per workgroup (each paired with a second KV
+        // wavefront): 4 shares every staged K/V tile among 128 query rows;
+        // hd 128 uses 2 to stay within 256 VGPRs, and so do small grids
         const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
-        int waves = wg4 >= 256 ? 4 : 2;
+        int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
         if (c->waves_override == 2 || c->waves_override == 4) waves = c->waves_override;
         e = vxfa::launch_prefill(a, (int)D, waves, st);
     }
