@@ -33,6 +33,7 @@ struct AttnArgs {
     int32_t nq, nkv, hq, hkv, b, bk, hm, bm;
     int32_t q_f16;        // q element type is f16
     int32_t n_split;      // decode: workgroups per (batch, kv head)
+    int32_t mask_vec;     // mask data and strides 16-byte aligned (128-bit mask loads)
     float scale_log2;     // scale * log2(e)
 };
 

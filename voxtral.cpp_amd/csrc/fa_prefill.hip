@@ -9,22 +9,40 @@
 // Work decomposition
 //   One workgroup per (block of BM = 32 * NQW query rows, query head, batch)
 //   with NQW * KVG wavefronts: wavefront (qw, kg) owns query rows
-//   [32 qw, 32 qw + 32) of the block and the kg-th 64-position half of every
-//   128-position KV step (KVG = 2). The two KV halves give each SIMD two
-//   independent wavefronts, so one's softmax (VALU) runs beside the other's
-//   MFMAs; they are merged through LDS at the end.
+//   [32 qw, 32 qw + 32) of the block and the kg-th 64-position tile of every
+//   KV step of BS = 64 * KVG positions. With hd 64 a workgroup has 16
+//   wavefronts, 4 per SIMD, so while some run their softmax (VALU) the
+//   others keep the matrix pipe busy. The KVG partial results are merged
+//   through LDS at the end (log-sum-exp).
 //   The 1-D grid is mapped so the workgroups that share one head's K/V are
 //   dispatched to the same XCD (workgroups are dealt to the 8 XCDs round
 //   robin), keeping that head's K/V in one L2. Without a mask each workgroup
-//   starts its KV walk at an offset set by its query block, so the workgroups
-//   of one head do not all miss on the same tile at once.
-// Pipeline: K/V steps are double buffered in LDS; the step after next is in
-//   flight in registers; one barrier per step.
+//   starts its KV walk at a step set by its query block, so the workgroups of
+//   one head do not all miss on the same tile at once.
+// Pipeline: K/V steps are double buffered in LDS and filled straight from
+//   global memory with global_load_lds_dwordx4 (no staging registers), the
+//   next step streaming in while the current one is computed; one barrier
+//   per step. The loads are issued through inline assembly: the compiler
+//   then neither orders the reads of one stage after the loads into the
+//   other (it cannot tell the stages apart inside one array) nor counts them,
+//   and each wavefront waits for its own loads (s_waitcnt vmcnt(0)) right
+//   before the step's barrier.
+// LDS rows are unpadded, row-major [kv][d], with the 16-byte chunks of each
+//   row XOR-swizzled: chunk c of row r sits at position c ^ f(r). Unswizzled,
+//   the K-operand reads (16 rows, one chunk) hit the same banks 8-fold (hd 64)
+//   or 16-fold (hd 128). Measured on gfx950 with 16 wavefronts per CU, these
+//   f make the K reads (ds_read_b128) and the V^T reads (8-byte transposed
+//   reads) conflict-free:
+//     hd 64 :  K f(r) = (r ^ r >> 2) & 7,          V f(r) = (r & 2) << 1
+//     hd 128:  K f(r) = (r >> 1 ^ r << 2) & 15,    V f(r) = (r & 3) << 2
+//   None depends on row bits 5 and up, so rows 32 apart share the swizzle,
+//   and the V swizzles depend on the row's position in its 4-row group only:
+//   every LDS read address is a lane constant plus an immediate.
 // MFMA layouts (v_mfma_f32_32x32x16_f16, lane = 32*hh + nl):
 //   S^T = K Q^T: A = K rows from LDS (128-bit reads), B = Q (registers, f16
 //     rounded like ggml's Q conversion). Lane (nl, hh) receives query row nl
-//     and 16 contiguous KV positions of each 32-block, so the row max needs
-//     one cross-lane step (v_permlane32_swap).
+//     and 16 KV positions of each 32-block, so the row max needs one
+//     cross-lane step (v_permlane32_swap).
 //   O^T = V^T P^T: B = P straight from the softmax registers (f16), A = V^T
 //     fetched from the row-major V tile with ds_read_b64_tr_b16, which
 //     transposes 16-bit elements across each 16-lane group.
@@ -34,10 +52,8 @@
 // Row-to-KV mapping inside a 32-position block (lane half hh, accumulator
 // element j, a = j / 4, b = j % 4):
 //   hh = 0 : kv = 4a + b            hh = 1 : kv = 16 + 4((a + 2) & 3) + b
-// so that (1) the K rows one 16-lane LDS phase reads fall in 16 distinct
-// bank groups with a 16-byte row padding, and (2) each half of a lane's
-// accumulator (j < 8, j >= 8) covers 8 contiguous positions in increasing
-// order, the order the P.V operand needs.
+// so that each half of a lane's accumulator (j < 8, j >= 8) covers 8
+// contiguous positions in increasing order, the order the P.V operand needs.
 #include "fa_common.h"
 
 #include <type_traits>
@@ -46,7 +62,7 @@ namespace vxfa {
 
 constexpr int PF_BN = 64;                // KV positions per wavefront tile
 constexpr float PF_TAU = 8.0f;
-constexpr int PF_MAX_TILE_WORDS = 256;   // live-tile bitmap: up to 8192 tiles
+constexpr int PF_MAX_STEP_WORDS = 256;   // live-step bitmap: up to 8192 steps
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
@@ -54,13 +70,41 @@ __device__ __forceinline__ int pf_kv_of(int hh, int j) {
     return hh ? 16 + (((j >> 2) + 2) & 3) * 4 + (j & 3) : j;
 }
 
+// chunk swizzles of the K and V tiles in LDS (r = row within the step)
+template <int D>
+__device__ __forceinline__ int swz_k(int r) {
+    return D == 64 ? ((r ^ (r >> 2)) & 7) : (((r >> 1) ^ (r << 2)) & 15);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
+    return D == 64 ? ((r & 2) << 1) : ((r & 3) << 2);
+}
+
 // Four 16-bit elements, transposed across each 16-lane group: lane i of the
 // group receives element (i % 4) of the 8 bytes addressed by lane 4r + i/4,
 // for r = 0..3 (gfx950 ds_read_b64_tr_b16).
-__device__ __forceinline__ half4 lds_read_tr16(const _Float16* p) {
+__device__ __forceinline__ half4 lds_read_tr16(const char* p) {
     const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(p));
     return __builtin_bit_cast(half4, r);
 }
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
+// at LDS offset lds + 16 * l (lds wave-uniform, in M0). Global address:
+// uniform base + 32-bit lane offset, or a full 64-bit lane address.
+__device__ __forceinline__ void dma16(const char* base, uint32_t off, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma16_addr(const char* addr, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
+}
+
+// wait for every outstanding memory operation of this wavefront
+// (s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0))
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 // max / sum over the lane pair (l, l ^ 32): v_permlane32_swap(x, x) returns
 // {x[l % 32], x[l % 32 + 32]} in every lane
@@ -78,23 +122,26 @@ __device__ __forceinline__ float pair32_sum(float x) {
 template <int D, int NQW, int KVG, bool MASK, bool QF16>
 __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, int nqt) {
     static_assert(D == 64 || D == 128, "head dim");
-    static_assert(KVG == 1 || KVG == 2, "kv groups");
-    constexpr int NT = 64 * NQW * KVG;
+    constexpr int NW = NQW * KVG;      // wavefronts
+    constexpr int NT = 64 * NW;
     constexpr int BM = 32 * NQW;
     constexpr int BS = PF_BN * KVG;    // KV positions per step
-    constexpr int KSTR = D + 8;        // halfs per K row in LDS: odd number of 16-byte units
-    constexpr int VSTR = D + 16;       // halfs per V row in LDS: the 4 rows of a tr-read hit distinct banks
     constexpr int KS = D / 16;         // S-MFMA k-steps
     constexpr int DB = D / 32;         // O^T row blocks
     constexpr int CH = D / 8;          // 16-byte chunks per row
-    constexpr int NCH = BS * CH / NT;  // chunks per thread per step (K and V each)
-    static_assert(NCH * NT == BS * CH, "step split");
-    constexpr int KBYTES = BS * KSTR * 2, VBYTES = BS * VSTR * 2;
+    constexpr int ROWS_PER_LOAD = 64 / CH;   // rows one wavefront instruction fills
+    constexpr int NLOAD = BS * CH / NT;      // instructions per wavefront per matrix per step
+    static_assert(NLOAD * NT == BS * CH, "step split");
+    constexpr int TILE_BYTES = BS * D * 2;   // one matrix of one step
+    constexpr int NE = 16 * DB;              // O elements per lane
+    constexpr int XSLOT = NQW * 64;          // floats per published O element
+    static_assert((KVG - 1) * NE * XSLOT * 4 <= 4 * TILE_BYTES, "merge buffers");
 
-    __shared__ __attribute__((aligned(16))) char smem[2 * (KBYTES + VBYTES)];
-    __shared__ uint32_t s_live[MASK ? PF_MAX_TILE_WORDS : 1];
-    auto sK = [&](int st) { return (_Float16*)(smem + st * (KBYTES + VBYTES)); };
-    auto sV = [&](int st) { return (_Float16*)(smem + st * (KBYTES + VBYTES) + KBYTES); };
+    // V first: its reads (twice as many as K's) then need no base register
+    __shared__ __attribute__((aligned(16))) char sV[2 * TILE_BYTES];
+    __shared__ __attribute__((aligned(16))) char sK[2 * TILE_BYTES];
+    __shared__ float s_ml[KVG > 1 ? 2 * (KVG - 1) * NQW * 64 : 1];
+    __shared__ uint32_t s_live[MASK ? PF_MAX_STEP_WORDS : 1];
 
     // ---- XCD-aware position of this workgroup --------------------------------
     const int nwg = gridDim.x;
@@ -107,7 +154,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int qw = wave % NQW;
     const int kg = wave / NQW;
     const int q0 = qt * BM;
@@ -120,52 +167,65 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     const int hh = lane >> 5;
     const int qrow = q0 + qw * 32 + nl;
     const bool qvalid = qrow < a.nq;
-    const int ntile = (a.nkv + PF_BN - 1) / PF_BN;   // 64-position tiles
     const int nstep = (a.nkv + BS - 1) / BS;         // BS-position steps
 
-    // ---- live tiles of the mask for this workgroup's rows -----------------
+    // ---- live steps of the mask for this workgroup's rows -------------------
+    // 16-byte mask loads when the mask allows them; each lane marks the step
+    // of its 8 positions (BS is a multiple of 8).
     const uint16_t* mplane = nullptr;
     bool use_bitmap = false;
     if (MASK) {
         mplane = (const uint16_t*)((const char*)a.mask + (int64_t)(h % a.hm) * a.m_nb2 +
                                    (int64_t)(b % a.bm) * a.m_nb3);
-        const int words = (ntile + 31) / 32;
-        use_bitmap = words <= PF_MAX_TILE_WORDS;
+        const int words = (nstep + 31) / 32;
+        use_bitmap = words <= PF_MAX_STEP_WORDS;
         if (use_bitmap) {
             for (int i = tid; i < words; i += NT) s_live[i] = 0u;
             __syncthreads();
             const int rows = min(BM, a.nq - q0);
-            for (int r = 0; r < rows; ++r) {
-                const uint16_t* mr = (const uint16_t*)((const char*)mplane + (int64_t)(q0 + r) * a.m_nb1);
-                for (int cc = tid; cc < a.nkv; cc += NT) {
+            if (a.mask_vec) {
+                const int n8 = (a.nkv + 7) / 8;   // 8-position groups per row
+                for (int i = tid; i < rows * n8; i += NT) {
+                    const int r = i / n8, g8 = i % n8;
+                    const uint16_t* mr = (const uint16_t*)((const char*)mplane + (int64_t)(q0 + r) * a.m_nb1);
+                    bool live = false;
+                    if (8 * g8 + 8 <= a.nkv) {
+                        const u32x4 w = *(const u32x4*)(mr + 8 * g8);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) live |= w[e] != 0xFC00FC00u;
+                    } else {
+                        for (int cc = 8 * g8; cc < a.nkv; ++cc) live |= mr[cc] != kF16NegInf;
+                    }
+                    if (live) {
+                        const int st = (8 * g8) / BS;
+                        atomicOr(&s_live[st >> 5], 1u << (st & 31));
+                    }
+                }
+            } else {
+                for (int i = tid; i < rows * a.nkv; i += NT) {
+                    const int r = i / a.nkv, cc = i % a.nkv;
+                    const uint16_t* mr = (const uint16_t*)((const char*)mplane + (int64_t)(q0 + r) * a.m_nb1);
                     if (mr[cc] != kF16NegInf) {
-                        const int tile = cc / PF_BN;
-                        const uint32_t bit = 1u << (tile & 31);
-                        if (!(s_live[tile >> 5] & bit)) atomicOr(&s_live[tile >> 5], bit);
+                        const int st = cc / BS;
+                        atomicOr(&s_live[st >> 5], 1u << (st & 31));
                     }
                 }
             }
             __syncthreads();
         }
     }
-    // Step sequence: without a mask all steps, rotated by the query block;
-    // with a mask the steps holding a live tile, in order. -1 ends it.
+    // Step sequence. Without a mask: every step, the last one (which holds
+    // the partial tile when n_kv % 64 != 0) last, the others rotated by the
+    // query block. With a mask: the steps holding a live position, in order.
+    // -1 ends the sequence.
     const bool seq_all = !MASK || !use_bitmap;
-    const int rot = MASK ? 0 : (int)(((int64_t)qt * nstep) / nqt) % nstep;
-    auto step_live = [&](int s) -> bool {
-        bool live = false;
-#pragma unroll
-        for (int g = 0; g < KVG; ++g) {
-            const int t = s * KVG + g;
-            if (t < ntile && ((s_live[t >> 5] >> (t & 31)) & 1u)) live = true;
-        }
-        return live;
-    };
-    auto advance = [&](int s) -> int {
-        if (s < 0) return -1;
+    auto step_live = [&](int s) -> bool { return (s_live[s >> 5] >> (s & 31)) & 1u; };
+    int n_left = nstep - 1;   // steps after the current one (sequence of all steps)
+    auto next_step = [&](int s) -> int {
         if (seq_all) {
-            const int idx = (s - rot + nstep) % nstep + 1;
-            return idx < nstep ? (rot + idx) % nstep : -1;
+            if (n_left <= 0) return -1;
+            if (--n_left == 0) return nstep - 1;
+            return s + 2 == nstep ? 0 : s + 1;
         }
         for (int u = s + 1; u < nstep; ++u)
             if (step_live(u)) return u;
@@ -173,7 +233,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     };
     int first = -1;
     if (seq_all) {
-        first = rot;
+        first = (MASK || nstep == 1) ? 0 : (int)(((int64_t)qt * (nstep - 1)) / nqt);
     } else {
         for (int u = 0; u < nstep; ++u)
             if (step_live(u)) { first = u; break; }
@@ -193,26 +253,45 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         }
     }
 
-    // ---- step staging: global -> registers -> LDS (row-major K and V) -------
-    half8 rk[NCH], rv[NCH];
-    auto gload = [&](int s) {
+    // ---- step loads: global -> LDS ------------------------------------------
+    // Instruction i of wavefront w fills rows [ROWS_PER_LOAD * (w + NW i), + ROWS_PER_LOAD)
+    // of the step; lane l writes LDS chunk l % CH of row + l / CH, which holds
+    // the row's chunk (l % CH) ^ swizzle(row). A step's rows start at a scalar
+    // base; each lane adds a 32-bit offset fixed for the whole walk (row
+    // strides are below 8 MiB, checked by the host). The last step clamps
+    // rows past n_kv to row n_kv - 1 instead.
+    const int ld_row = lane / CH;
+    uint32_t ldk[NLOAD], ldv[NLOAD];
+    int colk[NLOAD], colv[NLOAD];
+#pragma unroll
+    for (int i = 0; i < NLOAD; ++i) {
+        const int r = ROWS_PER_LOAD * (wave + NW * i) + ld_row;
+        colk[i] = ((lane % CH) ^ swz_k<D>(r)) * 16;
+        colv[i] = ((lane % CH) ^ swz_v<D>(r)) * 16;
+        ldk[i] = (uint32_t)r * (uint32_t)a.k_nb1 + colk[i];
+        ldv[i] = (uint32_t)r * (uint32_t)a.v_nb1 + colv[i];
+    }
+    const uint32_t lds_k = lds_offset(sK), lds_v = lds_offset(sV);
+    auto issue_step = [&](int s, int stg) {
         const int kv0 = s * BS;
+        const uint32_t k_dst = lds_k + stg * TILE_BYTES, v_dst = lds_v + stg * TILE_BYTES;
+        if (kv0 + BS <= a.nkv) {
+            const char* kst = kb + (int64_t)kv0 * a.k_nb1;
+            const char* vst = vb + (int64_t)kv0 * a.v_nb1;
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int ci = tid + i * NT;
-            const int kv = min(kv0 + ci / CH, a.nkv - 1);
-            rk[i] = *(const half8*)(kb + (int64_t)kv * a.k_nb1 + (ci % CH) * 16);
-            rv[i] = *(const half8*)(vb + (int64_t)kv * a.v_nb1 + (ci % CH) * 16);
-        }
-    };
-    auto swrite = [&](int st) {
-        _Float16* k = sK(st);
-        _Float16* v = sV(st);
+            for (int i = 0; i < NLOAD; ++i) {
+                const uint32_t r0b = ROWS_PER_LOAD * (wave + NW * i) * D * 2;
+                dma16(kst, ldk[i], k_dst + r0b);
+                dma16(vst, ldv[i], v_dst + r0b);
+            }
+        } else {
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int ci = tid + i * NT;
-            *(half8*)&k[(ci / CH) * KSTR + (ci % CH) * 8] = rk[i];
-            *(half8*)&v[(ci / CH) * VSTR + (ci % CH) * 8] = rv[i];
+            for (int i = 0; i < NLOAD; ++i) {
+                const int r0 = ROWS_PER_LOAD * (wave + NW * i);
+                const int kv = min(kv0 + r0 + ld_row, a.nkv - 1);
+                dma16_addr(kb + (int64_t)kv * a.k_nb1 + colk[i], k_dst + r0 * D * 2);
+                dma16_addr(vb + (int64_t)kv * a.v_nb1 + colv[i], v_dst + r0 * D * 2);
+            }
         }
     };
 
@@ -223,78 +302,100 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         for (int j = 0; j < 16; ++j) o[db][j] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    // K row fetched by this lane as A-operand row nl of each 32-block (within
-    // this wavefront's 64-position tile of the step)
-    int krow0;
+    // K row this lane fetches as A-operand row nl of each 32-block, within this
+    // wavefront's 64-position tile of the step; kaddr[ks] = byte offset of its
+    // chunk 2 ks + hh (32-block kvb adds 32 rows, stage adds TILE_BYTES)
+    int kaddr[KS];
     {
         const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
-        krow0 = PF_BN * kg + (ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab);
+        const int krow = PF_BN * kg + (ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab);
+        const int kx = hh ^ swz_k<D>(krow);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kaddr[ks] = krow * D * 2 + ((2 * ks) ^ kx) * 16;
     }
-    // lane's element offset inside the V tile for the transposed reads: row
-    // (lane % 16) / 4 of a 4-row group, dims 16 * ((lane % 32) / 16) + 4 * (lane % 4)
-    const int v_lane_off = (PF_BN * kg + ((lane & 15) >> 2)) * VSTR + 16 * ((lane & 31) >> 4) + 4 * (lane & 3);
+    // V^T reads of operand pc = 2 kvb + cc: lane reads row kvl + 4 hi + vq of
+    // the tile, vq = (lane % 16) / 4, kvl = 32 kvb + (hh ? 24 - 8 cc : 8 cc) (the
+    // 8 positions of P operand pc), and the 8 bytes at dims 32 db + 16 ((lane %
+    // 32) / 16) + 4 (lane % 4), i.e. chunk 4 db + clo, clo = 2 ((lane % 32) / 16)
+    // + (lane % 4) / 2. vaddr[cc][db] = byte offset for kvb = 0, hi = 0.
+    int vaddr[2][DB];
+    {
+        const int vq = (lane & 15) >> 2;
+        const int clo = 2 * ((lane & 31) >> 4) + ((lane & 3) >> 1);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                vaddr[cc][db] = (PF_BN * kg + (hh ? 24 - 8 * cc : 8 * cc) + vq) * D * 2 +
+                                ((4 * db + clo) ^ swz_v<D>(vq)) * 16 + (lane & 1) * 8;
+    }
+    // mask row of this lane's query (rows past n_q read row 0: their results
+    // are never stored)
     const uint16_t* mrow = nullptr;
     if (MASK) mrow = (const uint16_t*)((const char*)mplane + (int64_t)(qvalid ? qrow : 0) * a.m_nb1);
     const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     const float c = a.scale_log2;
 
-    // one 64-position tile at kv0 from LDS stage st.
+    // Mask of the tile at kv0, as f16 pairs: element j of score block kvb is
+    // half (j % 2) of mw[kvb][j / 2]. Lane half 0 holds positions 32 kvb +
+    // 0..15 in order; lane half 1 holds 32 kvb + 16 + ((j + 8) % 16), the
+    // row-to-KV mapping, so its two 16-byte loads come swapped. Positions
+    // past n_kv read as -inf.
+    auto load_mask = [&](int kv0, uint32_t (&mw)[2][8]) {
+        if (a.mask_vec && kv0 + PF_BN <= a.nkv) {
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb) {
+                const uint16_t* p = mrow + kv0 + 32 * kvb + 16 * hh;
+                const u32x4 lo = *(const u32x4*)(p + 8 * hh);
+                const u32x4 hi = *(const u32x4*)(p + 8 - 8 * hh);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    mw[kvb][w] = lo[w];
+                    mw[kvb][4 + w] = hi[w];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                for (int w = 0; w < 8; ++w) {
+                    uint32_t pair = 0;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int kv = kv0 + 32 * kvb + pf_kv_of(hh, 2 * w + e);
+                        const uint32_t bits = kv < a.nkv ? mrow[kv] : kF16NegInf;
+                        pair |= bits << (16 * e);
+                    }
+                    mw[kvb][w] = pair;
+                }
+        }
+    };
+
+    // One 64-position tile at kv0 from LDS stage stg.
     // TAIL: the tile runs past n_kv (positions >= n_kv are forced to -inf).
-    auto tile = [&](auto tail_tag, int st, int kv0) {
-        constexpr bool TAIL = decltype(tail_tag)::value;
-        float mv[2][16];
-        bool live = true;
-        if (MASK) {
+    auto tile = [&](auto tail_tag, int stg, int kv0, const uint32_t (&mw)[2][8]) {
+        constexpr bool TAIL = !MASK && decltype(tail_tag)::value;   // the mask path covers the tail
+        if constexpr (MASK) {
             bool any = false;
 #pragma unroll
             for (int kvb = 0; kvb < 2; ++kvb)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int kv = kv0 + 32 * kvb + pf_kv_of(hh, j);
-                    float m = -INFINITY;
-                    if (qvalid && kv < a.nkv) m = f16_bits_to_f32(mrow[kv]);
-                    mv[kvb][j] = m * kLog2e;
-                    any |= (m != -INFINITY);
-                }
-            live = __any(any);
+                for (int w = 0; w < 8; ++w) any |= mw[kvb][w] != 0xFC00FC00u;
+            if (!__any(any)) return;
         }
-        if (!live) return;
+        const char* ks_ = sK + stg * TILE_BYTES;
+        const char* vs_ = sV + stg * TILE_BYTES;
 
-        // hd 64: every LDS operand of the tile is requested up front, so the
-        // V^T reads complete behind the S MFMAs and the softmax instead of
-        // stalling P.V (hd 128 has no registers to spare and reads V^T late).
-        constexpr bool HOIST = (D == 64);
-        const _Float16* ks_ = sK(st);
-        const _Float16* vs = sV(st) + v_lane_off;
-        auto read_va = [&](int pc, int db) -> half8 {
-            // the 8 positions of operand pc, increasing from kvl
-            const int kvl = 32 * (pc >> 1) + (hh ? 16 + 8 * (1 - (pc & 1)) : 8 * (pc & 1));
-            const _Float16* p = vs + kvl * VSTR + 32 * db;
-            const half4 lo4 = lds_read_tr16(p);
-            const half4 hi4 = lds_read_tr16(p + 4 * VSTR);
-            return half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-        };
-        half8 ka[2][KS];
-#pragma unroll
-        for (int kvb = 0; kvb < 2; ++kvb)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                ka[kvb][ks] = *(const half8*)&ks_[(32 * kvb + krow0) * KSTR + 16 * ks + 8 * hh];
-        half8 va[HOIST ? 4 : 1][DB];
-        if constexpr (HOIST) {
-#pragma unroll
-            for (int pc = 0; pc < 4; ++pc)
-#pragma unroll
-                for (int db = 0; db < DB; ++db) va[pc][db] = read_va(pc, db);
-        }
         floatx16 S[2];
 #pragma unroll
         for (int kvb = 0; kvb < 2; ++kvb) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) S[kvb][j] = 0.f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                S[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kvb][ks], qb[ks], S[kvb], 0, 0, 0);
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 ka = *(const half8*)(ks_ + kaddr[ks] + 32 * kvb * D * 2);
+                S[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], S[kvb], 0, 0, 0);
+            }
         }
 
         // Row max in log2 units. Without a mask the scale is applied after the
@@ -308,7 +409,10 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     float x = S[kvb][j] * c;
-                    if (MASK) x = (mv[kvb][j] == -INFINITY) ? -INFINITY : x + mv[kvb][j];
+                    if constexpr (MASK) {
+                        const half2 m2 = __builtin_bit_cast(half2, mw[kvb][j >> 1]);
+                        x = fmaf((float)m2[j & 1], kLog2e, x);   // -inf stays -inf
+                    }
                     if (TAIL && kv0 + 32 * kvb + pf_kv_of(hh, j) >= a.nkv) x = -INFINITY;
                     S[kvb][j] = x;
                     mx = fmaxf(mx, x);
@@ -360,65 +464,106 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
             }
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const half8 vop = HOIST ? va[HOIST ? pc : 0][db] : read_va(pc, db);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pb, o[db], 0, 0, 0);
+                const char* p = vs_ + vaddr[cc][db] + 32 * kvb * D * 2;
+                const half4 lo4 = lds_read_tr16(p);
+                const half4 hi4 = lds_read_tr16(p + 4 * D * 2);
+                const half8 va = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[db], 0, 0, 0);
             }
         }
         l_run += lsum[0] + lsum[1];
     };
 
-    // ---- main loop: step s in stage st; step s_next staged at the top of the
-    // iteration; step s_next2 in flight in registers -----------------------------
-    int s_cur = first;
-    int s_nxt = advance(s_cur);
-    int s_nx2 = advance(s_nxt);
-    if (s_cur >= 0) { gload(s_cur); swrite(0); }
-    if (s_nxt >= 0) gload(s_nxt);
-    __syncthreads();
-    int st = 0;
-    while (s_cur >= 0) {
-        // the other stage was last read in the previous iteration, before its barrier
-        if (s_nxt >= 0) swrite(st ^ 1);
-        if (s_nx2 >= 0) gload(s_nx2);
-        const int kv0 = s_cur * BS + PF_BN * kg;
-        if (kv0 < a.nkv) {
-            if (kv0 + PF_BN > a.nkv) tile(std::true_type{}, st, kv0);
-            else tile(std::false_type{}, st, kv0);
+    // One step: start loading step s_nxt into stage STG ^ 1 (and, under a
+    // mask, the mask words of its tile), compute step s_cur from stage STG
+    // (full tiles, or any tile under a mask), then wait for the loads and for
+    // every wavefront. The stage is a template constant so every LDS read
+    // address is a register plus an immediate.
+    uint32_t mwa[2][8], mwb[2][8];
+    auto run_step = [&](auto stg_tag, int s_cur, int s_nxt, const uint32_t (&mw_cur)[2][8], uint32_t (&mw_nxt)[2][8]) {
+        constexpr int STG = decltype(stg_tag)::value;
+        if (s_nxt >= 0) {
+            issue_step(s_nxt, STG ^ 1);
+            const int kv0n = s_nxt * BS + PF_BN * kg;
+            if (MASK && kv0n < a.nkv) load_mask(kv0n, mw_nxt);
         }
+        const int kv0 = s_cur * BS + PF_BN * kg;
+        if (kv0 < a.nkv) tile(std::false_type{}, STG, kv0, mw_cur);
+        wait_all_mem();
         __syncthreads();
+    };
+
+    // Stage 0 and stage 1 alternate. Without a mask the last step of the
+    // sequence (it may hold the partial tile) is left for after the loop.
+    int s_cur = first;
+    int last_stage = 0;
+    if (s_cur >= 0) {
+        issue_step(s_cur, 0);
+        const int kv0 = s_cur * BS + PF_BN * kg;
+        if (MASK && kv0 < a.nkv) load_mask(kv0, mwa);
+    }
+    wait_all_mem();
+    __syncthreads();
+    while (s_cur >= 0) {
+        int s_nxt = next_step(s_cur);
+        if (!MASK && s_nxt < 0) { last_stage = 0; break; }
+        run_step(std::integral_constant<int, 0>{}, s_cur, s_nxt, mwa, mwb);
         s_cur = s_nxt;
-        s_nxt = s_nx2;
-        s_nx2 = advance(s_nx2);
-        st ^= 1;
+        if (s_cur < 0) break;
+        s_nxt = next_step(s_cur);
+        if (!MASK && s_nxt < 0) { last_stage = 1; break; }
+        run_step(std::integral_constant<int, 1>{}, s_cur, s_nxt, mwb, mwa);
+        s_cur = s_nxt;
+    }
+    if (!MASK && s_cur >= 0) {
+        const int kv0 = s_cur * BS + PF_BN * kg;
+        if (kv0 < a.nkv) tile(std::true_type{}, last_stage, kv0, mwa);   // mask words unused
+        __syncthreads();
     }
 
     // ---- merge the KV groups (LDS), normalise, store dst[b][qrow][h][d] ------
-    if (KVG == 2) {
-        // group 1 publishes (m, l, O); every staging buffer is free after the
-        // loop's last barrier
-        float* xo = (float*)smem;                          // [NQW][64 lanes][16 * DB]
-        float* xm = xo + NQW * 64 * 16 * DB;               // [NQW][64]
-        float* xl = xm + NQW * 64;
-        if (kg == 1) {
+    if constexpr (KVG > 1) {
+        // groups 1.. publish (m, l, O) element-major, so a wavefront's 64
+        // lanes write consecutive words; the stage arrays are free after the
+        // last barrier. Element e of group g goes to slot (g - 1) * NE + e of
+        // XSLOT floats, filling sV and then sK.
+        constexpr int SLOTS_V = 2 * TILE_BYTES / (XSLOT * 4);
+        const int slot = qw * 64 + lane;
+        auto xo_at = [&](int g, int e) -> float* {
+            const int L = (g - 1) * NE + e;
+            return L < SLOTS_V ? (float*)sV + L * XSLOT + slot : (float*)sK + (L - SLOTS_V) * XSLOT + slot;
+        };
+        float* xm = s_ml;
+        float* xl = s_ml + (KVG - 1) * NQW * 64;
+        if (kg > 0) {
 #pragma unroll
             for (int db = 0; db < DB; ++db)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) xo[(qw * 64 + lane) * 16 * DB + db * 16 + j] = o[db][j];
-            xm[qw * 64 + lane] = m_run;
-            xl[qw * 64 + lane] = l_run;
+                for (int j = 0; j < 16; ++j) *xo_at(kg, db * 16 + j) = o[db][j];
+            xm[(kg - 1) * NQW * 64 + slot] = m_run;
+            xl[(kg - 1) * NQW * 64 + slot] = l_run;
         }
         __syncthreads();
-        if (kg == 1) return;
-        const float m2 = xm[qw * 64 + lane], l2 = xl[qw * 64 + lane];
-        const float M = fmaxf(m_run, m2);
+        if (kg > 0) return;
+        float M = m_run;
+#pragma unroll
+        for (int g = 1; g < KVG; ++g) M = fmaxf(M, xm[(g - 1) * NQW * 64 + slot]);
         const float Ms = (M == -INFINITY) ? 0.f : M;
-        const float w1 = exp2_fast(m_run - Ms), w2 = exp2_fast(m2 - Ms);
-        l_run = l_run * w1 + l2 * w2;
+        const float w0 = exp2_fast(m_run - Ms);
+        l_run *= w0;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                o[db][j] = o[db][j] * w1 + xo[(qw * 64 + lane) * 16 * DB + db * 16 + j] * w2;
+            for (int j = 0; j < 16; ++j) o[db][j] *= w0;
+#pragma unroll
+        for (int g = 1; g < KVG; ++g) {
+            const float wg = exp2_fast(xm[(g - 1) * NQW * 64 + slot] - Ms);
+            l_run = fmaf(wg, xl[(g - 1) * NQW * 64 + slot], l_run);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) o[db][j] = fmaf(wg, *xo_at(g, db * 16 + j), o[db][j]);
+        }
     }
     const float lt = pair32_sum(l_run);
     const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
@@ -436,7 +581,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     }
 }
 
-template <int D, int NQW, int KVG>
+template <int D, int NQW, int KVG, bool MASK>
 static hipError_t launch_pw(const AttnArgs& a, hipStream_t st) {
     constexpr int BM = 32 * NQW;
     const int nqt = (a.nq + BM - 1) / BM;
@@ -444,25 +589,24 @@ static hipError_t launch_pw(const AttnArgs& a, hipStream_t st) {
     if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
     constexpr int NT = 64 * NQW * KVG;
     const dim3 grid((unsigned)nwg), block(NT);
-    if (a.mask) {
-        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, true, true>), grid, block, 0, st, a, nqt);
-        else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, true, false>), grid, block, 0, st, a, nqt);
-    } else {
-        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, false, true>), grid, block, 0, st, a, nqt);
-        else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, false, false>), grid, block, 0, st, a, nqt);
-    }
+    if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MASK, true>), grid, block, 0, st, a, nqt);
+    else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MASK, false>), grid, block, 0, st, a, nqt);
     return hipGetLastError();
 }
 
-// waves = query-row wavefronts per workgroup (32 rows each); each has a
-// partner wavefront for the second KV half.
+// waves = query-row wavefronts per workgroup (32 rows each); 0 picks the
+// default. hd 64 without a mask: 4 (16 wavefronts with their 3 KV partners,
+// 4 per SIMD) or 2. hd 64 with a mask keeps its mask words in registers and
+// always runs 2 (8 wavefronts). hd 128: 4 or 2 with one KV partner each.
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t st) {
+    const bool mask = a.mask != nullptr;
     if (head_dim == 64) {
-        if (waves == 4) return launch_pw<64, 4, 2>(a, st);
-        if (waves == 2) return launch_pw<64, 2, 2>(a, st);
+        if (mask) return launch_pw<64, 2, 4, true>(a, st);
+        if (waves == 0 || waves == 4) return launch_pw<64, 4, 4, false>(a, st);
+        if (waves == 2) return launch_pw<64, 2, 4, false>(a, st);
     } else if (head_dim == 128) {
-        if (waves == 4) return launch_pw<128, 4, 2>(a, st);
-        if (waves == 2) return launch_pw<128, 2, 2>(a, st);
+        if (waves == 0 || waves == 4) return mask ? launch_pw<128, 4, 2, true>(a, st) : launch_pw<128, 4, 2, false>(a, st);
+        if (waves == 2) return mask ? launch_pw<128, 2, 2, true>(a, st) : launch_pw<128, 2, 2, false>(a, st);
     }
     return hipErrorInvalidValue;
 }

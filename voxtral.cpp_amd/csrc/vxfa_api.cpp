@@ -100,6 +100,12 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
         *why = "sizes beyond the launch limits";
         return VXFA_UNSUPPORTED;
     }
+    // the prefill kernel addresses up to 256 K/V rows from one base with
+    // 32-bit offsets
+    if (k->nb[1] >= ((size_t)1 << 23) || v->nb[1] >= ((size_t)1 << 23)) {
+        *why = "k/v row stride must be below 8 MiB";
+        return VXFA_UNSUPPORTED;
+    }
     // 128-bit loads: q/k/v rows and dst rows must be 16-byte aligned
     const vxfa_tensor* vec[4] = {q, k, v, dst};
     for (int i = 0; i < 4; ++i) {
@@ -219,6 +225,8 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
     a.hm = mask ? (int32_t)mask->ne[2] : 1;
     a.bm = mask ? (int32_t)mask->ne[3] : 1;
     a.q_f16 = q->type == VXFA_TYPE_F16;
+    a.mask_vec = mask && aligned16(mask->data, 0) && !(mask->nb[1] & 15) && !(mask->nb[2] & 15) &&
+                 !(mask->nb[3] & 15);
     a.scale_log2 = scale * vxfa::kLog2e;
 
     const int64_t G = Hq / Hkv;
@@ -247,9 +255,9 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
         }
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
-        // query-row wavefronts per workgroup (each paired with a second KV
-        // wavefront): 4 shares every staged K/V tile among 128 query rows;
-        // hd 128 uses 2 to stay within 256 VGPRs, and so do small grids
+        // query-row wavefronts per workgroup (each with its KV partner
+        // wavefronts): 4 shares every staged K/V step among 128 query rows;
+        // hd 128 and small grids (fewer than 128 workgroups of 128 rows) use 2
         const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
         int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
         if (c->waves_override == 2 || c->waves_override == 4) waves = c->waves_override;
