@@ -1,0 +1,127 @@
+"""The C ABI without a GPU: libvxfa.so loads, exports every function that
+include/vxfa.h declares, and its host-only capability check (the supports_op
+analogue) accepts voxtral.cpp's views and rejects what the path does not do.
+No call here launches work or touches a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import cases
+from conftest import ROOT, load_package
+
+vxfa = load_package().vxfa
+views = load_package().views
+
+HEADER = os.path.join(ROOT, "include", "vxfa.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vxfa_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_what_the_binding_binds():
+    assert declared_functions() == sorted(vxfa.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = vxfa.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_version_and_status_strings():
+    lib = vxfa.load()
+    assert lib.vxfa_version() >= 10000
+    for s in (vxfa.OK, vxfa.UNSUPPORTED, vxfa.INVALID_ARG, vxfa.NO_WORKSPACE, vxfa.HIP_ERROR):
+        assert lib.vxfa_status_str(s).decode() not in ("", "unknown status")
+    assert lib.vxfa_status_str(99).decode() == "unknown status"
+    assert lib.vxfa_last_error(None).decode() == ""
+
+
+def test_struct_layout_matches_header():
+    # void* data; int32 type; int32 pad_; int64 ne[4]; size_t nb[4]
+    assert ctypes.sizeof(vxfa.VxfaTensor) == 8 + 4 + 4 + 32 + 32
+    assert vxfa.VxfaTensor.ne.offset == 16 and vxfa.VxfaTensor.nb.offset == 48
+
+
+ADDR = 1 << 20   # a 16-byte aligned fake device address: supports() never dereferences it
+
+
+def descs(c):
+    d = {}
+    for role, (b, t, ne, nb, off) in c.views.items():
+        d[role] = vxfa.desc(ADDR + off, t, ne, nb)
+    B, Nq, Hq, D = c.out_shape
+    d["dst"] = vxfa.desc(ADDR, vxfa.F32, *views.dst(D, Hq, Nq, B))
+    return d
+
+
+def supports(c, **over):
+    d = descs(c)
+    d.update({k: v for k, v in over.items() if k in d or k == "mask"})
+    return vxfa.supports(d["q"], d["k"], d["v"], d.get("mask"), d["dst"], c.scale,
+                         over.get("max_bias", 0.0), over.get("softcap", 0.0))
+
+
+@pytest.mark.parametrize("make", [
+    lambda: cases.decode_case(1024, seed=1),
+    lambda: cases.decode_case(100, seed=1, window=10),
+    lambda: cases.encoder_case(64, 20, 64, seed=1),
+    lambda: cases.prefill_case(40, seed=1),
+    lambda: cases.batched_case(4, capacity=64, lo=2, hi=64, seed=1),
+])
+def test_voxtral_views_are_supported(make):
+    assert supports(make()) == vxfa.OK
+
+
+def test_unsupported_features_report_unsupported():
+    c = cases.decode_case(64, seed=2)
+    assert supports(c, max_bias=8.0) == vxfa.UNSUPPORTED
+    assert supports(c, softcap=30.0) == vxfa.UNSUPPORTED
+    d = descs(c)
+    k32 = vxfa.desc(ADDR, vxfa.F32, d["k"].ne, [4, 4096, 512, 4096 * 64])
+    assert vxfa.supports(d["q"], k32, d["v"], None, d["dst"], c.scale) == vxfa.UNSUPPORTED
+    # head dim 96 is a valid op but not one this path implements
+    c96 = cases.decode_case(64, hq=4, hkv=1, hd=96, seed=3)
+    assert supports(c96) == vxfa.UNSUPPORTED
+
+
+def test_contract_violations_report_invalid():
+    c = cases.decode_case(64, hq=8, hkv=2, seed=4)
+    d = descs(c)
+    bad_k = vxfa.desc(ADDR, vxfa.F16, (128, 64, 3, 1), d["k"].nb)          # 8 % 3 != 0
+    bad_v = vxfa.desc(ADDR, vxfa.F16, (128, 63, 2, 1), d["v"].nb)          # n_kv mismatch
+    bad_dst = vxfa.desc(ADDR, vxfa.F32, (128, 1, 8, 1), (4, 512, 512, 4096))  # not permuted
+    assert vxfa.supports(d["q"], bad_k, d["v"], None, d["dst"], c.scale) == vxfa.INVALID_ARG
+    assert vxfa.supports(d["q"], d["k"], bad_v, None, d["dst"], c.scale) == vxfa.INVALID_ARG
+    assert vxfa.supports(d["q"], d["k"], d["v"], None, bad_dst, c.scale) == vxfa.INVALID_ARG
+    short_mask = vxfa.desc(ADDR, vxfa.F16, (63, 1, 1, 1), (2, 126, 126, 126))
+    assert vxfa.supports(d["q"], d["k"], d["v"], short_mask, d["dst"], c.scale) == vxfa.INVALID_ARG
+    assert vxfa.supports(None, d["k"], d["v"], None, d["dst"], c.scale) == vxfa.INVALID_ARG
+
+
+def test_unaligned_views_are_unsupported_not_invalid():
+    c = cases.decode_case(64, seed=5)
+    d = descs(c)
+    q_odd = vxfa.desc(ADDR + 4, vxfa.F32, d["q"].ne, d["q"].nb)
+    assert vxfa.supports(q_odd, d["k"], d["v"], None, d["dst"], c.scale) == vxfa.UNSUPPORTED
+
+
+def test_unpadded_odd_mask_rows_are_accepted():
+    """voxtral passes an unpadded [n, n] mask (src/voxtral.cpp:2024, :1880):
+    439-wide rows are 878 bytes, not 16-byte aligned."""
+    c = cases.prefill_case(439, seed=6)
+    assert c.views["mask"][3][1] == 878
+    assert supports(c) == vxfa.OK
+
+
+def test_zero_sized_query_is_accepted():
+    c = cases.decode_case(16, seed=7)
+    b, t, ne, nb, off = c.views["q"]
+    c.views["q"] = (b, t, (ne[0], ne[1], ne[2], 0), nb, off)
+    assert supports(c) == vxfa.OK

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import cases
+import golden_util
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -111,6 +112,20 @@ def test_batched_ragged_32_streams(runner):
     c = cases.batched_case(32, seed=17)
     _say(f"    lengths {c.meta['lens'].tolist()}")
     check_case(runner, c)
+
+
+# --- the committed fixtures (expected = torch float64 SDPA) --------------------
+
+@pytest.mark.parametrize("name", golden_util.names())
+def test_golden_fixture(runner, name):
+    import gpu_util
+    c, want = golden_util.load(name)
+    _say(f"[golden] {name}")
+    rc, out = runner.run(c)
+    assert rc == 0
+    m, r, ok = gpu_util.parity(out, want, ATOL, RTOL)
+    _say(f"    maxabs={m:.3e} rel={r:.3e}")
+    assert ok, (m, r)
 
 
 # --- contract edge cases --------------------------------------------------------
