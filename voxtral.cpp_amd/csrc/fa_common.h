@@ -87,6 +87,94 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
+// Eight consecutive F16 mask entries starting at p, as four 32-bit words
+// (entry e in half e % 2 of word e / 2). Entries at or past `valid` read as
+// -inf. The widest load the address allows is used: 16, 4 or 2 bytes.
+__device__ __forceinline__ u32x4 load_mask8(const uint16_t* p, int valid) {
+    const uint32_t dead = 0xFC00FC00u;
+    u32x4 w = {dead, dead, dead, dead};
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+    if (valid >= 8 && (addr & 15) == 0) {
+        w = *reinterpret_cast<const u32x4*>(p);
+    } else if (valid >= 8 && (addr & 3) == 0) {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+        w = u32x4{q[0], q[1], q[2], q[3]};
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t h = e < valid ? (uint32_t)p[e] : (uint32_t)kF16NegInf;
+            w[e >> 1] = (e & 1) ? ((w[e >> 1] & 0xFFFFu) | (h << 16)) : ((w[e >> 1] & 0xFFFF0000u) | h);
+        }
+    }
+    return w;
+}
+
+// Bit e set when entry e of the eight is not -inf.
+__device__ __forceinline__ uint32_t live_bits8(u32x4 w) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m |= ((w[i] & 0xFFFFu) != kF16NegInf ? 1u : 0u) << (2 * i);
+        m |= ((w[i] >> 16) != kF16NegInf ? 1u : 0u) << (2 * i + 1);
+    }
+    return m;
+}
+
+// Live range [lo, hi) over `rows` mask rows of n entries each (row r at
+// base + r * row_stride bytes): lo is the first and hi - 1 the last column
+// holding an entry other than -inf in any of the rows; lo = hi = 0 when every
+// entry is -inf. Every thread of the block calls it and gets the result.
+// Rows are cut into 8-entry chunks; each thread takes whole chunks, four at a
+// time with all loads issued before any test, so the scan costs a few memory
+// round trips whatever the row alignment. red: 2 ints of LDS per wavefront.
+template <int NT>
+__device__ __forceinline__ void mask_live_range(const uint16_t* base, int64_t row_stride, int rows, int n, int* red,
+                                                int& lo, int& hi) {
+    const int tid = threadIdx.x;
+    const int nch = (n + 7) >> 3;
+    const int items = rows * nch;
+    int tlo = 0x7fffffff, thi = -1;
+    for (int i0 = tid; i0 < items; i0 += 4 * NT) {
+        u32x4 w[4];
+        int col[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * NT;
+            col[u] = -1;
+            w[u] = u32x4{0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u};
+            if (i < items) {
+                const int r = i / nch, c = i - r * nch;
+                col[u] = 8 * c;
+                const uint16_t* p = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) +
+                                                                      (int64_t)r * row_stride) + 8 * c;
+                w[u] = load_mask8(p, n - 8 * c);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t m = live_bits8(w[u]);
+            if (m) {
+                tlo = min(tlo, col[u] + (int)__builtin_ctz(m));
+                thi = max(thi, col[u] + 31 - (int)__builtin_clz(m));
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        tlo = min(tlo, __shfl_xor(tlo, off, 64));
+        thi = max(thi, __shfl_xor(thi, off, 64));
+    }
+    const int wave = tid >> 6;
+    if ((tid & 63) == 0) { red[2 * wave] = tlo; red[2 * wave + 1] = thi; }
+    __syncthreads();
+    tlo = red[0];
+    thi = red[1];
+#pragma unroll
+    for (int wv = 1; wv < NT / 64; ++wv) { tlo = min(tlo, red[2 * wv]); thi = max(thi, red[2 * wv + 1]); }
+    __syncthreads();   // red may be reused by the caller
+    if (thi < 0) { lo = 0; hi = 0; } else { lo = tlo; hi = thi + 1; }
+}
+
 }  // namespace vxfa
 
 // Host-side launchers (implemented in the kernel translation units).

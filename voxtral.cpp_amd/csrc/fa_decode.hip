@@ -10,8 +10,9 @@
 //   fa_decode_split   grid (n_split, Hkv, B), 4 wavefronts per workgroup.
 //                     Each workgroup reduces one contiguous slice of the live
 //                     KV range to (O, m, l) per query head of its group.
-//   fa_decode_combine grid (Hkv, B): log-sum-exp merge of the n_split
-//                     partials in a fixed order (deterministic output).
+//   fa_decode_combine grid (Hkv * G, B): log-sum-exp merge of the n_split
+//                     partials of one query head, in a fixed order
+//                     (deterministic output).
 // With n_split == 1 the split kernel writes the output and no merge runs.
 // The kernel boundary orders the partials' stores before the merge's loads;
 // an in-kernel last-block merge needs an agent-scope release fence (an L2
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     __shared__ float lds_acc[DEC_WAVES][G][D];
     __shared__ float lds_m[DEC_WAVES][G];
     __shared__ float lds_l[DEC_WAVES][G];
-    __shared__ int lds_lo[DEC_WAVES], lds_hi[DEC_WAVES];
+    __shared__ int lds_red[2 * DEC_WAVES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -67,30 +68,27 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
 
     // ---- live range of the KV axis -------------------------------------
+    // The mask rows of this group's query heads: planes (g G + j) % hm of
+    // batch b % bm. One scan when they are one plane or consecutive planes.
     int lo = 0, hi = a.nkv;
     if constexpr (masked) {
-        int tlo = 0x7fffffff, thi = -1;
-        const int nplanes = (a.hm == 1) ? 1 : G;
-        for (int j = 0; j < nplanes; ++j) {
-            const int hq = g * G + j;
-            const uint16_t* mrow = (const uint16_t*)((const char*)a.mask + (int64_t)(hq % a.hm) * a.m_nb2 +
-                                                     (int64_t)(b % a.bm) * a.m_nb3);
-            for (int i = tid; i < a.nkv; i += DEC_THREADS) {
-                if (mrow[i] != kF16NegInf) {
-                    tlo = min(tlo, i);
-                    thi = max(thi, i);
-                }
+        const char* mb = (const char*)a.mask + (int64_t)(b % a.bm) * a.m_nb3;
+        const int p0 = (g * G) % a.hm;
+        const int np = a.hm == 1 ? 1 : (p0 + G <= a.hm ? G : 0);
+        if (np > 0) {
+            mask_live_range<DEC_THREADS>((const uint16_t*)(mb + (int64_t)p0 * a.m_nb2), a.m_nb2, np, a.nkv, lds_red,
+                                         lo, hi);
+        } else {
+            lo = 0x7fffffff;
+            hi = 0;
+            for (int j = 0; j < G; ++j) {
+                int l1, h1;
+                mask_live_range<DEC_THREADS>((const uint16_t*)(mb + (int64_t)((g * G + j) % a.hm) * a.m_nb2), 0, 1,
+                                             a.nkv, lds_red, l1, h1);
+                if (h1 > l1) { lo = min(lo, l1); hi = max(hi, h1); }
             }
+            if (hi == 0) lo = 0;
         }
-        for (int off = 32; off >= 1; off >>= 1) {
-            tlo = min(tlo, __shfl_xor(tlo, off, 64));
-            thi = max(thi, __shfl_xor(thi, off, 64));
-        }
-        if (lane == 0) { lds_lo[wave] = tlo; lds_hi[wave] = thi; }
-        __syncthreads();
-        tlo = lds_lo[0]; thi = lds_hi[0];
-        for (int w = 1; w < DEC_WAVES; ++w) { tlo = min(tlo, lds_lo[w]); thi = max(thi, lds_hi[w]); }
-        if (thi < 0) { lo = 0; hi = 0; } else { lo = tlo; hi = thi + 1; }
     }
 
     const int span = hi - lo;
@@ -300,73 +298,76 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     }
 }
 
-// Log-sum-exp merge of the n_split partial records of one (kv head, batch):
+// Log-sum-exp merge of the n_split partial records of one query head:
 //   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
-// All loads are independent, so the merge costs about two round trips.
+// Grid (Hkv * G, B): one workgroup per query head. The O partials are loaded
+// first (their addresses do not depend on the weights), then wavefront 0
+// loads the n_split (m, l) pairs, one per lane, and forms the weights with
+// wavefront reductions; the whole merge costs one memory round trip. The
+// summation order is fixed, so the output is deterministic.
 template <int D, int G>
 __global__ __launch_bounds__(DEC_THREADS) void fa_decode_combine(AttnArgs a) {
-    constexpr int NF = G * D / 4;                 // float4 outputs
-    constexpr int NPART = DEC_THREADS / NF;       // threads per output
-    static_assert(NPART >= 1 && NF * NPART == DEC_THREADS, "combine split");
-    __shared__ float cw[kDecodeMaxSplit * G];
-    __shared__ float cm[kDecodeMaxSplit * G];
-    __shared__ float cl[kDecodeMaxSplit * G];
-    __shared__ float cL[G];
-    __shared__ floatx4 cpart[NPART][NF];
+    constexpr int NF4 = D / 4;                    // float4 per head row
+    constexpr int NGRP = DEC_THREADS / NF4;       // split groups
+    constexpr int MAXS = kDecodeMaxSplit / NGRP;  // splits per thread
+    static_assert(NGRP * NF4 == DEC_THREADS && MAXS * NGRP == kDecodeMaxSplit, "combine split");
+    static_assert(kDecodeMaxSplit == 64, "one (m, l) pair per lane of wavefront 0");
+    __shared__ float cw[kDecodeMaxSplit];
+    __shared__ float cL;
+    __shared__ floatx4 cpart[NGRP][NF4];
 
     const int tid = threadIdx.x;
-    const int g = blockIdx.x;
+    const int g = blockIdx.x / G, h = blockIdx.x % G;
     const int b = blockIdx.y;
     const int rs = G * (D + 2);
-    const float* base = a.ws + (int64_t)(b * a.hkv + g) * a.n_split * rs;
-    const int nsg = a.n_split * G;
-    for (int i = tid; i < nsg; i += DEC_THREADS) {
-        const int s = i / G, h = i % G;
-        cm[i] = base[(int64_t)s * rs + G * D + h];
-        cl[i] = base[(int64_t)s * rs + G * D + G + h];
-    }
-    __syncthreads();
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, cm[s * G + tid]);
-        const float Ms = (M == -INFINITY) ? 0.f : M;
-        float L = 0.f;
-        for (int s = 0; s < a.n_split; ++s) {
-            const float w = exp2_fast(cm[s * G + tid] - Ms);
-            cw[s * G + tid] = w;
-            L = fmaf(w, cl[s * G + tid], L);
-        }
-        cL[tid] = L;
-    }
-    __syncthreads();
-    {
-        const int f = tid % NF, part = tid / NF;
-        const int h = (4 * f) / D;
-        floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 16
-        for (int sp = part; sp < a.n_split; sp += NPART) {
-            const floatx4 x = *(const floatx4*)(base + (int64_t)sp * rs + 4 * f);
-            const float w = cw[sp * G + h];
-            acc4[0] = fmaf(w, x[0], acc4[0]);
-            acc4[1] = fmaf(w, x[1], acc4[1]);
-            acc4[2] = fmaf(w, x[2], acc4[2]);
-            acc4[3] = fmaf(w, x[3], acc4[3]);
-        }
-        cpart[part][f] = acc4;
-    }
-    __syncthreads();
-    if (tid < NF) {
-        floatx4 acc4 = cpart[0][tid];
+    const int ns = a.n_split;
+    const float* base = a.ws + (int64_t)(b * a.hkv + g) * ns * rs;
+    const int f = tid % NF4, grp = tid / NF4;
+
+    floatx4 o[MAXS];
 #pragma unroll
-        for (int p = 1; p < NPART; ++p) {
+    for (int i = 0; i < MAXS; ++i) {
+        const int sp = grp + i * NGRP;
+        o[i] = sp < ns ? *(const floatx4*)(base + (int64_t)sp * rs + h * D + 4 * f) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (tid < 64) {
+        const float m = tid < ns ? base[(int64_t)tid * rs + G * D + h] : -INFINITY;
+        const float l = tid < ns ? base[(int64_t)tid * rs + G * D + G + h] : 0.f;
+        float M = m;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+        const float Ms = (M == -INFINITY) ? 0.f : M;
+        const float w = exp2_fast(m - Ms);        // 0 for an empty split (m = -inf)
+        float L = w * l;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
+        cw[tid] = w;
+        if (tid == 0) cL = L;
+    }
+    __syncthreads();
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+        const int sp = grp + i * NGRP;
+        const float w = sp < ns ? cw[sp] : 0.f;
+        acc[0] = fmaf(w, o[i][0], acc[0]);
+        acc[1] = fmaf(w, o[i][1], acc[1]);
+        acc[2] = fmaf(w, o[i][2], acc[2]);
+        acc[3] = fmaf(w, o[i][3], acc[3]);
+    }
+    cpart[grp][f] = acc;
+    __syncthreads();
+    if (tid < NF4) {
+        floatx4 s = cpart[0][tid];
+#pragma unroll
+        for (int p = 1; p < NGRP; ++p) {
             const floatx4 y = cpart[p][tid];
-            acc4[0] += y[0]; acc4[1] += y[1]; acc4[2] += y[2]; acc4[3] += y[3];
+            s[0] += y[0]; s[1] += y[1]; s[2] += y[2]; s[3] += y[3];
         }
-        const int h = (4 * tid) / D, d = (4 * tid) % D;
-        const float L = cL[h];
+        const float L = cL;
         const float inv = (L == 0.f) ? 0.f : 1.0f / L;
-        floatx4 out = {acc4[0] * inv, acc4[1] * inv, acc4[2] * inv, acc4[3] * inv};
-        *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G + h) * D + d) = out;
+        const floatx4 out = {s[0] * inv, s[1] * inv, s[2] * inv, s[3] * inv};
+        *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G + h) * D + 4 * tid) = out;
     }
 }
 
@@ -381,7 +382,7 @@ static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
         else hipLaunchKernelGGL((fa_decode_split<D, G, false, false>), grid, block, 0, st, a);
     }
     if (a.n_split > 1)
-        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv, a.b), dim3(DEC_THREADS), 0, st, a);
+        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G, a.b), dim3(DEC_THREADS), 0, st, a);
     return hipGetLastError();
 }
 

@@ -62,7 +62,6 @@ namespace vxfa {
 
 constexpr int PF_BN = 64;                // KV positions per wavefront tile
 constexpr float PF_TAU = 8.0f;
-constexpr int PF_MAX_STEP_WORDS = 256;   // live-step bitmap: up to 8192 steps
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
@@ -141,7 +140,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     __shared__ __attribute__((aligned(16))) char sV[2 * TILE_BYTES];
     __shared__ __attribute__((aligned(16))) char sK[2 * TILE_BYTES];
     __shared__ float s_ml[KVG > 1 ? 2 * (KVG - 1) * NQW * 64 : 1];
-    __shared__ uint32_t s_live[MASK ? PF_MAX_STEP_WORDS : 1];
+    __shared__ int s_red[2 * NW];
 
     // ---- XCD-aware position of this workgroup --------------------------------
     const int nwg = gridDim.x;
@@ -169,75 +168,37 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     const bool qvalid = qrow < a.nq;
     const int nstep = (a.nkv + BS - 1) / BS;         // BS-position steps
 
-    // ---- live steps of the mask for this workgroup's rows -------------------
-    // 16-byte mask loads when the mask allows them; each lane marks the step
-    // of its 8 positions (BS is a multiple of 8).
+    // ---- live column range of the mask over this workgroup's rows -----------
+    // Steps wholly outside the range are never loaded; a tile inside it whose
+    // mask entries are all -inf is skipped after its load (tile()).
     const uint16_t* mplane = nullptr;
-    bool use_bitmap = false;
+    int step_lo = 0, step_hi = nstep;
     if (MASK) {
         mplane = (const uint16_t*)((const char*)a.mask + (int64_t)(h % a.hm) * a.m_nb2 +
                                    (int64_t)(b % a.bm) * a.m_nb3);
-        const int words = (nstep + 31) / 32;
-        use_bitmap = words <= PF_MAX_STEP_WORDS;
-        if (use_bitmap) {
-            for (int i = tid; i < words; i += NT) s_live[i] = 0u;
-            __syncthreads();
-            const int rows = min(BM, a.nq - q0);
-            if (a.mask_vec) {
-                const int n8 = (a.nkv + 7) / 8;   // 8-position groups per row
-                for (int i = tid; i < rows * n8; i += NT) {
-                    const int r = i / n8, g8 = i % n8;
-                    const uint16_t* mr = (const uint16_t*)((const char*)mplane + (int64_t)(q0 + r) * a.m_nb1);
-                    bool live = false;
-                    if (8 * g8 + 8 <= a.nkv) {
-                        const u32x4 w = *(const u32x4*)(mr + 8 * g8);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) live |= w[e] != 0xFC00FC00u;
-                    } else {
-                        for (int cc = 8 * g8; cc < a.nkv; ++cc) live |= mr[cc] != kF16NegInf;
-                    }
-                    if (live) {
-                        const int st = (8 * g8) / BS;
-                        atomicOr(&s_live[st >> 5], 1u << (st & 31));
-                    }
-                }
-            } else {
-                for (int i = tid; i < rows * a.nkv; i += NT) {
-                    const int r = i / a.nkv, cc = i % a.nkv;
-                    const uint16_t* mr = (const uint16_t*)((const char*)mplane + (int64_t)(q0 + r) * a.m_nb1);
-                    if (mr[cc] != kF16NegInf) {
-                        const int st = cc / BS;
-                        atomicOr(&s_live[st >> 5], 1u << (st & 31));
-                    }
-                }
-            }
-            __syncthreads();
-        }
+        int lo = 0, hi = 0;
+        const int rows = min(BM, a.nq - q0);
+        mask_live_range<NT>((const uint16_t*)((const char*)mplane + (int64_t)q0 * a.m_nb1), a.m_nb1, rows, a.nkv,
+                            s_red, lo, hi);
+        step_lo = lo / BS;
+        step_hi = hi > lo ? (hi - 1) / BS + 1 : 0;
     }
     // Step sequence. Without a mask: every step, the last one (which holds
     // the partial tile when n_kv % 64 != 0) last, the others rotated by the
-    // query block. With a mask: the steps holding a live position, in order.
+    // query block. With a mask: the steps of the live range, in order.
     // -1 ends the sequence.
-    const bool seq_all = !MASK || !use_bitmap;
-    auto step_live = [&](int s) -> bool { return (s_live[s >> 5] >> (s & 31)) & 1u; };
     int n_left = nstep - 1;   // steps after the current one (sequence of all steps)
     auto next_step = [&](int s) -> int {
-        if (seq_all) {
+        if (!MASK) {
             if (n_left <= 0) return -1;
             if (--n_left == 0) return nstep - 1;
             return s + 2 == nstep ? 0 : s + 1;
         }
-        for (int u = s + 1; u < nstep; ++u)
-            if (step_live(u)) return u;
-        return -1;
+        return s + 1 < step_hi ? s + 1 : -1;
     };
     int first = -1;
-    if (seq_all) {
-        first = (MASK || nstep == 1) ? 0 : (int)(((int64_t)qt * (nstep - 1)) / nqt);
-    } else {
-        for (int u = 0; u < nstep; ++u)
-            if (step_live(u)) { first = u; break; }
-    }
+    if (!MASK) first = nstep == 1 ? 0 : (int)(((int64_t)qt * (nstep - 1)) / nqt);
+    else if (step_lo < step_hi) first = step_lo;
 
     // ---- Q operand (B of S^T = K Q^T): row qrow, dims 16ks + 8hh .. +7 ----
     // (the Q element type is a template parameter: a load-or-convert branch on
