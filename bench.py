@@ -30,6 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 
 MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense f16/bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+HEADLINE_KERNEL = "fa_prefill_kernel<64"
 METRIC = "attn µs/layer; prefill TFLOP/s % MFMA peak; decode HBM GB/s % peak @1 GPU"
 
 
@@ -192,28 +193,59 @@ def decode_bytes(n_live, hq=32, hkv=8, hd=128, mask_bytes=0):
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle), bounded sample
 
-def cpu_baseline_encoder(seq=1500, heads=20, hd=64):
-    """One full encoder layer through the ggml-faithful CPU restatement."""
+def cpu_baseline_encoder(seq=1500, heads=20, hd=64, layers=5):
+    """`layers` encoder layers (about 10 s on 16 host cores) through the
+    ggml-faithful CPU restatement, each on its own seeded inputs."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle
-    rng = np.random.default_rng(7)
-    q = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).astype(np.float32)
-    k = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
-    v = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
-    qv = oracle.View(q, oracle.F32, *views.encoder_qkv(seq, heads, hd, 4))
-    kv = oracle.View(k, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2))
-    vv = oracle.View(v, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2))
     threads = oracle.default_threads()
-    oracle.fa_ggml(qv, kv, vv, None, 0.125, vkq_f16=True, threads=threads)  # warm-up (small, same code)
+    views_ = []
+    for i in range(layers):
+        rng = np.random.default_rng(7 + i)
+        q = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).astype(np.float32)
+        k = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
+        views_.append((oracle.View(q, oracle.F32, *views.encoder_qkv(seq, heads, hd, 4)),
+                       oracle.View(k, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)),
+                       oracle.View(v, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2))))
     t0 = time.perf_counter()
-    oracle.fa_ggml(qv, kv, vv, None, 0.125, vkq_f16=True, threads=threads)
+    for qv, kv, vv in views_:
+        oracle.fa_ggml(qv, kv, vv, None, 0.125, vkq_f16=True, threads=threads)
     dt = time.perf_counter() - t0
-    flops = 4.0 * seq * seq * hd * heads
+    flops = 4.0 * seq * seq * hd * heads * layers
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"1 encoder layer (1500x1500, 20 heads, hd64) through oracle/fa_oracle.c "
-                      f"(ggml one-row algorithm, f16 V accumulation), {dt:.2f} s",
-            "us_per_layer": dt * 1e6}
+            "sample": f"{layers} encoder layers (1500x1500, 20 heads, hd64, distinct seeded inputs) through "
+                      f"oracle/fa_oracle.c (ggml one-row algorithm, f16 V accumulation), {dt:.2f} s",
+            "us_per_layer": dt / layers * 1e6}
+
+
+def load_traffic(kernel_prefix):
+    """HBM bytes per launch of the headline kernel, from the committed PMC
+    profile (profiles/encoder_prefill_traffic.json): FETCH_SIZE + WRITE_SIZE
+    per dispatch, each scaled by the same counter's reading for a copy kernel
+    of known size. None when the profile is absent or names another kernel."""
+    path = os.path.join(ROOT, "profiles", "encoder_prefill_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if not str(t.get("kernel", "")).startswith(kernel_prefix):
+        return None
+    return t.get("hbm_bytes_per_launch")
+
+
+def calib_copy(torch, mib=256, reps=3):
+    """A plain copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
+    counters in a PMC run (each copy reads and writes `mib` MiB)."""
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"[calib] copied {mib} MiB x {reps}")
 
 
 def cpu_decode_us(n_kv=8192):
@@ -245,6 +277,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of configs to run (debug)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 256 MiB copy kernel (counter calibration for PMC runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -375,12 +409,16 @@ def main():
                                "k/v f16), no mask, scale 1/8, 32 layers per step",
                    "global_batch": 1, "seq_len": 1500, "heads": 20, "head_dim": 64, "layers": 32},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "fa_prefill_kernel<64,4,false>", "us_per_launch": us_layer},
+                     "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic(HEADLINE_KERNEL),
+                     "kernel": "fa_prefill_kernel<64, 4, 4, false, false>", "us_per_launch": us_layer,
+                     "traffic_unit": "bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "algorithmic_bytes": 2 * 1500 * 20 * 64 * 2 + 2 * 1500 * 20 * 64 * 4},
         "cpu_baseline": cpu,
         "configs": configs,
     }
     print(json.dumps(line), flush=True)
+    if args.calib_copy:
+        calib_copy(torch)
     ctx.close()
 
 
