@@ -30,7 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 
 MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense f16/bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
-HEADLINE_KERNEL = "fa_prefill_kernel<64"
+HEADLINE_KERNEL = "fa_prefill64_pp"
 METRIC = "attn µs/layer; prefill TFLOP/s % MFMA peak; decode HBM GB/s % peak @1 GPU"
 
 
@@ -410,7 +410,7 @@ def main():
                    "global_batch": 1, "seq_len": 1500, "heads": 20, "head_dim": 64, "layers": 32},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic(HEADLINE_KERNEL),
-                     "kernel": "fa_prefill_kernel<64, 4, 4, false, false>", "us_per_launch": us_layer,
+                     "kernel": "fa_prefill64_pp<Shape<2, 4, 4>, false, true>", "us_per_launch": us_layer,
                      "traffic_unit": "bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "algorithmic_bytes": 2 * 1500 * 20 * 64 * 2 + 2 * 1500 * 20 * 64 * 4},
         "cpu_baseline": cpu,

@@ -98,18 +98,27 @@ def _batched_q(n_tokens, heads, hd, elt, batch):
     return (ne[0], ne[1], ne[2], batch), (nb[0], nb[1], nb[2], n_tokens * heads * hd * elt)
 
 
-def encoder_case(seq=1500, heads=20, hd=64, seed=2, name=None, window=None):
+def encoder_case(seq=1500, heads=20, hd=64, seed=2, name=None, window=None, scale=None, q_f16=False,
+                 k_ramp=0.0, q_sigma=1.0):
     """Encoder self-attention (src/voxtral.cpp:1580-1613): q/k/v [hd, seq, heads]
     views of [seq][heads][hd] buffers. q is f16-valued, stored as F32 (the
-    reference's q is a mul_mat output); window: realtime sliding-causal mask
-    (src/voxtral.cpp:2179-2190)."""
+    reference's q is a mul_mat output) or, with q_f16, as F16; window: realtime
+    sliding-causal mask (src/voxtral.cpp:2179-2190). k_ramp > 0 scales key row
+    j by 1 + k_ramp * j / seq, so row maxima keep growing along the KV axis.
+    scale defaults to 1/sqrt(hd)."""
     rng = np.random.default_rng(seed)
-    c = Case(name or f"encoder_seq{seq}", f32(1.0 / math.sqrt(hd)))
-    qh = f16_bits(normal(rng, (seq, heads, hd)))
+    c = Case(name or f"encoder_seq{seq}", f32(1.0 / math.sqrt(hd) if scale is None else scale))
+    qh = f16_bits(normal(rng, (seq, heads, hd), q_sigma))
     q = qh.view(np.float16).astype(np.float32)
-    k = f16_bits(normal(rng, (seq, heads, hd)))
+    kf = normal(rng, (seq, heads, hd))
+    if k_ramp:
+        kf = kf * (1.0 + k_ramp * np.arange(seq, dtype=np.float32) / seq)[:, None, None]
+    k = f16_bits(kf)
     v = f16_bits(normal(rng, (seq, heads, hd)))
-    c.add("q", "q", q, F32, *views.encoder_qkv(seq, heads, hd, 4))
+    if q_f16:
+        c.add("q", "q", qh, F16, *views.encoder_qkv(seq, heads, hd, 2))
+    else:
+        c.add("q", "q", q, F32, *views.encoder_qkv(seq, heads, hd, 4))
     c.add("k", "k", k, F16, *views.encoder_qkv(seq, heads, hd, 2))
     c.add("v", "v", v, F16, *views.encoder_qkv(seq, heads, hd, 2))
     if window is not None:

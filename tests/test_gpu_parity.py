@@ -163,6 +163,34 @@ def test_encoder_shapes(runner, seq):
     check_case(runner, cases.encoder_case(seq, 4, 64, seed=300 + seq))
 
 
+@pytest.mark.parametrize("seq", [32, 64, 96, 128, 161, 1024])
+def test_encoder_block_splits(runner, seq):
+    """hd 64 unmasked prefill: KV ranges that leave KV groups of a workgroup
+    empty (32, 64, 96), exact multiples of the 32-position block (no partial
+    block), and short groups next to full ones (161)."""
+    check_case(runner, cases.encoder_case(seq, 3, 64, seed=500 + seq))
+
+
+def test_encoder_rising_maxima(runner):
+    """Key norms grow along the KV axis (up to 5x), so the running row max is
+    raised in many blocks: the rescale path of the pipelined softmax."""
+    check_case(runner, cases.encoder_case(700, 4, 64, seed=26, k_ramp=4.0, q_sigma=2.0))
+
+
+def test_encoder_negative_and_f16_q(runner):
+    check_case(runner, cases.encoder_case(300, 4, 64, seed=27, scale=-0.125))
+    check_case(runner, cases.encoder_case(300, 4, 64, seed=28, q_f16=True))
+
+
+def test_encoder_zero_scale(runner):
+    """scale 0: every unmasked position weighs the same (mean of V)."""
+    check_case(runner, cases.encoder_case(200, 2, 64, seed=29, scale=0.0))
+
+
+def test_prefill_hd64_gqa_no_mask(runner):
+    check_case(runner, cases.prefill_case(257, hq=8, hkv=2, hd=64, causal=False, seed=30))
+
+
 def test_encoder_realtime_window(runner):
     """realtime encoder: sliding-causal window 750 (src/voxtral.cpp:2179-2190)"""
     check_case(runner, cases.encoder_case(1000, 4, 64, seed=24, window=750))

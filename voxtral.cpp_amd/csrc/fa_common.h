@@ -175,6 +175,68 @@ __device__ __forceinline__ void mask_live_range(const uint16_t* base, int64_t ro
     if (thi < 0) { lo = 0; hi = 0; } else { lo = tlo; hi = thi + 1; }
 }
 
+// ---- MFMA tile helpers shared by the prefill kernels ---------------------
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// KV position held by accumulator element j of lane half hh in a 32x32 S^T
+// block whose A-operand rows are the K rows permuted so that each half of a
+// lane's accumulator covers 8 contiguous positions, in increasing order:
+//   hh = 0 : kv = j            hh = 1 : kv = 16 + 4((j / 4 + 2) & 3) + j % 4
+__device__ __forceinline__ int pf_kv_of(int hh, int j) {
+    return hh ? 16 + (((j >> 2) + 2) & 3) * 4 + (j & 3) : j;
+}
+
+// chunk swizzles of the K and V tiles in LDS (r = row within the tile; only
+// bits 0-4 matter, so tiles of 32 or more rows share them)
+template <int D>
+__device__ __forceinline__ int swz_k(int r) {
+    return D == 64 ? ((r ^ (r >> 2)) & 7) : (((r >> 1) ^ (r << 2)) & 15);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
+    return D == 64 ? ((r & 2) << 1) : ((r & 3) << 2);
+}
+
+// Four 16-bit elements, transposed across each 16-lane group: lane i of the
+// group receives element (i % 4) of the 8 bytes addressed by lane 4r + i/4,
+// for r = 0..3 (gfx950 ds_read_b64_tr_b16).
+__device__ __forceinline__ half4 lds_read_tr16(const char* p) {
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(p));
+    return __builtin_bit_cast(half4, r);
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
+// at LDS offset lds + 16 * l (lds wave-uniform, in M0). Global address:
+// uniform base + 32-bit lane offset, or a full 64-bit lane address.
+__device__ __forceinline__ void dma16(const char* base, uint32_t off, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma16_addr(const char* addr, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
+}
+
+// wait for every outstanding memory operation of this wavefront
+// (s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0))
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// max / sum over the lane pair (l, l ^ 32): v_permlane32_swap(x, x) returns
+// {x[l % 32], x[l % 32 + 32]} in every lane
+__device__ __forceinline__ float pair32_max(float x) {
+    const int xi = __builtin_bit_cast(int, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+    const int xi = __builtin_bit_cast(int, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+    return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
+
 }  // namespace vxfa
 
 // Host-side launchers (implemented in the kernel translation units).
@@ -182,5 +244,6 @@ namespace vxfa {
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t stream);
 constexpr int kDecodeMaxSplit = 64;
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
+hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 }  // namespace vxfa

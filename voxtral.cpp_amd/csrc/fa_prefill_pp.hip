@@ -1,0 +1,591 @@
+// fa_prefill_pp.hip — encoder self-attention prefill (hd 64, no mask) for
+// gfx950: one wavefront per SIMD, software-pipelined so the matrix pipe and
+// the VALU overlap inside the wavefront.
+//
+// Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the offline
+// encoder call of voxtral.cpp: hd 64, 20 heads, 1500 frames, bidirectional,
+// mask = null, scale = 1/sqrt(64) (src/voxtral.cpp:1580-1613, FA at :1611).
+//
+// Work decomposition
+//   Workgroup = 2 query tiles of 64 rows x 2 KV groups = 4 wavefronts, one
+//   per SIMD. KV group g walks its own contiguous half of the 32-position
+//   blocks; the two groups' partial (O, m, l) are merged through LDS at the
+//   end. At 1500 x 20 the grid is 12 x 20 = 240 workgroups, one per CU. The
+//   workgroups of one head are dealt to one XCD (workgroups go to the 8 XCDs
+//   round robin), so that head's K/V stays in one L2.
+// Why 64 query rows per wavefront: every K and V operand read from LDS feeds
+//   two MFMAs (one per 32-row half), half the LDS reads per FLOP of a 32-row
+//   wavefront, whose operand reads alone would need the full LDS bandwidth
+//   at the MFMA peak.
+// Why one wavefront per SIMD: all its state (O, Q, S, P, K and V operands of
+//   both halves, ~230 VGPRs) stays in registers with no copies, and there is
+//   no second wavefront on the SIMD for the issue arbiter to favour.
+// Ping-pong inside the wavefront: the halves A (rows 0-31) and B (rows 32-63)
+//   run half an iteration apart. Iteration t (block t of the group):
+//     H1: MFMA  O_A += V_t^T P_A(t)^T, S_A(t+1) = K_{t+1} Q_A^T
+//         VALU  softmax of S_B(t) -> P_B(t)
+//     H2: MFMA  O_B += V_t^T P_B(t)^T, S_B(t+1) = K_{t+1} Q_B^T
+//         VALU  softmax of S_A(t+1) -> P_A(t+1)
+//   The MFMAs of a half do not depend on that half's VALU work, so the
+//   scheduler interleaves them. K_{t+1} and V_t are read at the top of
+//   iteration t; the softmax of S_B(t) needs neither, so the VALU (the
+//   busier pipe for hd 64) can start while the reads land.
+// K/V staging: an 8-slot LDS ring; block b sits in slot b % 8, its K is read
+//   at the top of iteration b - 1 and its V at the top of iteration b; block
+//   b + 7 goes into the slot of block b - 1 at the start of iteration b, one
+//   barrier after that block's last read (global_load_lds_dwordx4, no
+//   staging registers). A block therefore has five iterations to arrive; at
+//   the end of iteration t each wavefront waits only for its own loads of
+//   block t + 2 (s_waitcnt vmcnt counting the younger blocks still in
+//   flight), then one barrier.
+// Q is loaded coalesced by the whole workgroup, rounded to f16 and staged in
+//   LDS; the output goes out through LDS as full 256-byte rows.
+// LDS rows and swizzles, MFMA operand layouts and the row-to-KV permutation
+//   are those of fa_prefill.hip (measured conflict-free K and V^T reads).
+// Softmax in fp32 with exp2: x = c s - m is one FMA per score, the literal
+//   form v_fmamk_f32 when the scale is 1/8 (it issues at twice the rate of
+//   the three-register form). Inside the loop P is computed against the
+//   running max without reducing the block's max; the sum of P tells when a
+//   score passed that max by more than 2^8, and only then is the max raised
+//   (O and l rescaled) and P recomputed.
+#include "fa_common.h"
+
+#include <type_traits>
+
+namespace vxfa {
+
+namespace pp {
+constexpr int D = 64;
+constexpr int KS = D / 16;          // S-MFMA k-steps
+constexpr int DB = D / 32;          // O^T row blocks
+constexpr int BK = 32;              // KV positions per block
+constexpr int ROW = D * 2;          // bytes per K/V row
+constexpr int BLK = BK * ROW;       // bytes of one matrix block (4 KiB)
+constexpr int GRP = 2 * BLK;        // K then V of one group in a ring slot
+constexpr float TAU = 8.0f;
+
+// Workgroup shape: NQT query tiles of 64 rows x KVG KV groups (one wavefront
+// each), an NS-slot LDS ring.
+template <int NQT_, int KVG_, int NS_>
+struct Shape {
+    static constexpr int NQT = NQT_;
+    static constexpr int KVG = KVG_;
+    static constexpr int NS = NS_;
+    static constexpr int NW = NQT * KVG;        // wavefronts
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 64 * NQT;         // query rows per workgroup
+    static constexpr int AHEAD = NS - 1;        // blocks loaded ahead of the one computed
+    static constexpr int SLOT = KVG * GRP;
+    static constexpr int RING = NS * SLOT;
+    static constexpr int QST = BM * ROW;        // Q staging: BM rows of 64 f16
+    static constexpr int NLD = 4 / NQT;         // K (and V) load instructions per wavefront per block
+    static constexpr int PUB = 2 * 32 + 4;      // floats a merging wavefront publishes per lane
+    static constexpr int XS = (KVG - 1) * NQT * PUB * 64 * 4;   // merge area
+    static constexpr int OST = (XS + 255) / 256 * 256;        // output staging tile
+};
+// one wavefront per SIMD (4 wavefronts, 8-slot ring)
+using Shape1 = Shape<2, 2, 8>;
+// two wavefronts per SIMD (8 wavefronts, 4-slot ring)
+using Shape2 = Shape<2, 4, 4>;
+}  // namespace pp
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14, expcnt 7 and lgkmcnt
+// 15 mean "do not wait").
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// wait until at most k blocks' loads (2 NLD instructions each) are in flight
+template <int NLD>
+__device__ __forceinline__ void wait_blocks(int k) {
+    constexpr int L = 2 * NLD;
+    switch (k) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<L>(); break;
+        case 2: wait_vmcnt<2 * L>(); break;
+        case 3: wait_vmcnt<3 * L>(); break;
+        case 4: wait_vmcnt<4 * L>(); break;
+        case 5: wait_vmcnt<5 * L>(); break;
+        case 6: wait_vmcnt<6 * L>(); break;
+        case 7: wait_vmcnt<7 * L>(); break;
+        default: wait_vmcnt<8 * L>(); break;
+    }
+}
+
+template <class SH, bool QF16, bool C8>
+__global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, int nblk, int ni) {
+    using namespace pp;
+    constexpr int NQT = SH::NQT, KVG = SH::KVG, NS = SH::NS, NT = SH::NT, BM = SH::BM;
+    constexpr int AHEAD = SH::AHEAD, SLOT = SH::SLOT, RING = SH::RING, QST = SH::QST, NLD = SH::NLD;
+    static_assert(NLD * NQT == 4, "a block's 4 load instructions per matrix split evenly");
+    static_assert(8 * 2 * NLD < 64 && NS <= 8, "vmcnt range of wait_blocks");
+    static_assert(SH::OST + BM * 256 <= RING + QST, "merge and output staging fit the LDS");
+    __shared__ __attribute__((aligned(16))) char smem[RING + QST];
+
+    // ---- XCD-aware position of this workgroup --------------------------------
+    const int nwg = gridDim.x;
+    const int lin = blockIdx.x;
+    const int xcd = lin & 7, q8 = nwg >> 3, r8 = nwg & 7;
+    const int gidx = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + (lin >> 3);
+    const int qg = gidx % nqg;
+    const int h = (gidx / nqg) % a.hq;
+    const int b = gidx / (nqg * a.hq);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = wave / NQT;
+    const int wq = wave % NQT;
+    const int nl = lane & 31;
+    const int hh = lane >> 5;
+    const int qw0 = qg * BM;                  // first query row of the workgroup
+    const int hk = h / (a.hq / a.hkv);
+    const int bkv = b / (a.b / a.bk);
+    const float c = fabsf(a.scale_log2);      // |scale| * log2(e); a negative scale is folded into Q
+    const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
+    const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
+
+    // blocks [bs, bs + ng) of this KV group
+    const int bs = min(kg * ni, nblk);
+    const int ng = min(ni, nblk - bs);
+
+    // ---- Q: coalesced loads by the whole workgroup (issued first, so their
+    // latency overlaps the first K/V blocks) -----------------------------------
+    // Staged in LDS as f16 rows of 128 bytes, 16-byte chunk j of row r at
+    // position j ^ (r & 7). F32 Q: thread i takes 16-byte chunks i + NT u of
+    // the BM x 16 chunks; F16 Q: of the BM x 8 chunks.
+    constexpr int QCH = QF16 ? 8 : 16;         // 16-byte global chunks per row
+    constexpr int QPT = BM * QCH / NT;         // per thread
+    floatx4 qraw[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int i = tid + NT * u;
+        const int r = i / QCH, cch = i % QCH;
+        const int row = qw0 + r;
+        qraw[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (row < a.nq)
+            qraw[u] = *(const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 + (int64_t)h * a.q_nb2 +
+                                        (int64_t)b * a.q_nb3 + cch * 16);
+    }
+
+    // ---- block loads: global -> LDS ring -------------------------------------
+    // Instruction i of wavefront wq fills rows [8 (NQT i + wq), + 8) of the
+    // group's block; lane l writes LDS chunk l % 8 of row + l / 8, which holds
+    // the row's chunk (l % 8) ^ swizzle(row). A block's rows start at a
+    // scalar base plus a 32-bit lane offset (row strides are below 8 MiB,
+    // checked by the host); the partial last block clamps rows past n_kv to
+    // row n_kv - 1.
+    uint32_t ldk[NLD], ldv[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int r = 8 * (NQT * i + wq) + (lane >> 3);
+        ldk[i] = (uint32_t)r * (uint32_t)a.k_nb1 + ((lane & 7) ^ swz_k<D>(r)) * 16;
+        ldv[i] = (uint32_t)r * (uint32_t)a.v_nb1 + ((lane & 7) ^ swz_v<D>(r)) * 16;
+    }
+    const uint32_t lds0 = lds_offset(smem) + kg * GRP;
+    auto issue = [&](int blk) {   // blk: index within the group, < ng
+        const int kv0 = (bs + blk) * BK;
+        const uint32_t kd = lds0 + (blk % NS) * SLOT, vd = kd + BLK;
+        const char* kst = kb + (int64_t)kv0 * a.k_nb1;
+        const char* vst = vb + (int64_t)kv0 * a.v_nb1;
+        if (kv0 + BK <= a.nkv) {
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) {
+                const uint32_t r0b = 8 * (NQT * i + wq) * ROW;
+                dma16(kst, ldk[i], kd + r0b);
+                dma16(vst, ldv[i], vd + r0b);
+            }
+        } else {
+            // once per head: the offsets are recomputed here rather than held
+            // in registers across the loop (the empty asm keeps them here)
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int rmax = a.nkv - 1 - kv0;   // last valid row of the block (kv0 < n_kv)
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) {
+                const int r0 = 8 * (NQT * i + wq);
+                const int r = r0 + (ln >> 3);
+                const int rc = min(r, rmax);
+                dma16(kst, (uint32_t)rc * (uint32_t)a.k_nb1 + ((ln & 7) ^ swz_k<D>(r)) * 16, kd + r0 * ROW);
+                dma16(vst, (uint32_t)rc * (uint32_t)a.v_nb1 + ((ln & 7) ^ swz_v<D>(r)) * 16, vd + r0 * ROW);
+            }
+        }
+    };
+    const int npre = min(ng, AHEAD);
+    for (int blk = 0; blk < npre; ++blk) issue(blk);
+
+    // ---- Q: wait for its loads only, round to f16 (ggml's Q conversion, sign
+    // of the scale folded in), stage in LDS ------------------------------------
+    // (the npre blocks' loads were issued after the Q loads and may remain)
+    wait_blocks<NLD>(npre);
+    {
+        char* qs = smem + RING;
+        const float sg = a.scale_log2 < 0.f ? -1.0f : 1.0f;
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+            const int i = tid + NT * u;
+            const int r = i / QCH, cch = i % QCH;
+            if (QF16) {
+                const half8 v = __builtin_bit_cast(half8, qraw[u]) * (_Float16)sg;
+                *(half8*)(qs + r * ROW + ((cch ^ (r & 7)) * 16)) = v;
+            } else {
+                half4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = (_Float16)(qraw[u][e] * sg);
+                *(half4*)(qs + r * ROW + (((cch >> 1) ^ (r & 7)) * 16) + (cch & 1) * 8) = v;
+            }
+        }
+    }
+
+    // ---- operand reads from LDS (offsets within a group's block) ----------------
+    // K: A-operand row nl of the 32-block is K row krow (the row-to-KV
+    // permutation), chunk 2 ks + hh.
+    int kaddr[KS];
+    {
+        const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
+        const int krow = ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
+        const int kx = hh ^ swz_k<D>(krow);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kaddr[ks] = krow * ROW + ((2 * ks) ^ kx) * 16;
+    }
+    // V^T: operand (cc, db) covers the 8 positions of P operand cc, read as two
+    // transposed 8-byte loads 4 rows apart.
+    int vaddr[2][DB];
+    {
+        const int vq = (lane & 15) >> 2;
+        const int clo = 2 * ((lane & 31) >> 4) + ((lane & 3) >> 1);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                vaddr[cc][db] = ((hh ? 24 - 8 * cc : 8 * cc) + vq) * ROW + ((4 * db + clo) ^ swz_v<D>(vq)) * 16 +
+                                (lane & 1) * 8;
+    }
+    auto read_k = [&](int blk, half8 (&kr)[KS]) {
+        const char* base = smem + (blk % NS) * SLOT + kg * GRP;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kr[ks] = *(const half8*)(base + kaddr[ks]);
+    };
+    auto read_v = [&](int blk, half8 (&vr)[2][DB]) {
+        const char* base = smem + (blk % NS) * SLOT + kg * GRP + BLK;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const half4 lo4 = lds_read_tr16(base + vaddr[cc][db]);
+                const half4 hi4 = lds_read_tr16(base + vaddr[cc][db] + 4 * ROW);
+                vr[cc][db] = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            }
+    };
+
+    // ---- MFMA groups and the softmax -------------------------------------------
+    auto s_mfma = [&](floatx16& s, const half8 (&q)[KS], const half8 (&kr)[KS]) {
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[0], q[0], floatx16{}, 0, 0, 0);
+#pragma unroll
+        for (int ks = 1; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[ks], q[ks], s, 0, 0, 0);
+    };
+    auto pv_mfma = [&](floatx16 (&o)[DB], const half8 (&p)[2], const half8 (&vr)[2][DB]) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[cc][db], p[cc], o[db], 0, 0, 0);
+    };
+    // positions of the partial block blk at or past n_kv score -inf
+    auto tail_fix = [&](floatx16& sc, int blk) {
+        const int kv0 = (bs + blk) * BK;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (kv0 + pf_kv_of(hh, j) >= a.nkv) sc[j] = -INFINITY;
+    };
+    // P = 2^(c s - m) for the lane's 16 scores, as two f16 B operands, and
+    // their sum. With C8 (scale exactly 1/8) c is a literal and x = c s - m
+    // compiles to v_fmamk_f32, which issues at twice the rate of the
+    // three-register v_fma_f32; -m has to reach it as a plain register (a
+    // negation folded into the FMA would force the three-register form), so
+    // it passes through an empty asm. (Every instruction that reads an MFMA
+    // result must be one the compiler sees: it alone inserts the wait states
+    // such a read needs.)
+    const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    auto exps = [&](const floatx16& sc, float m, half8 (&p)[2]) -> float {
+        float nm = (m == -INFINITY) ? 0.f : -m;
+        asm("" : "+v"(nm));
+        float ls[2] = {0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                p[cc][i] = (_Float16)exp2_fast(fmaf(sc[8 * cc + i], C8 ? 0.18033688f : c, nm));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const half2 p2 = {p[cc][2 * i], p[cc][2 * i + 1]};
+                ls[i & 1] = __builtin_amdgcn_fdot2(p2, ones, ls[i & 1], false);
+            }
+        }
+        return ls[0] + ls[1];
+    };
+    // the block's max (log2 units) over the lane pair
+    auto block_max = [&](const floatx16& sc) -> float {
+        float r = sc[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) r = fmaxf(r, sc[j]);
+        return pair32_max(r) * c;
+    };
+    // raise the running max to mx: rescale O and l
+    auto raise = [&](float mx, float& m, float& l, floatx16 (&o)[DB]) {
+        const float mnew = fmaxf(m, mx);
+        const float ms = (mnew == -INFINITY) ? 0.f : mnew;
+        const float alpha = exp2_fast(m - ms);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
+        l *= alpha;
+        m = mnew;
+    };
+    // softmax of one block, max first (blocks outside the pipelined loop)
+    auto softmax_exact = [&](const floatx16& sc, float& m, float& l, floatx16 (&o)[DB], half8 (&p)[2]) {
+        const float mx = block_max(sc);
+        if (__any(mx > m + TAU)) raise(mx, m, l, o);
+        l += exps(sc, m, p);
+    };
+    // Softmax inside the pipelined loop. P is computed against the current
+    // running max m with no block max at all: a score more than TAU above m
+    // makes some P > 2^TAU, so the lane's sum of its 16 P exceeds 2^TAU (and is
+    // inf or NaN past the f16 range). Only then (rare once m has settled) is
+    // the block max reduced, O and l rescaled and P recomputed; a large sum of
+    // moderate P can also take that path, which is harmless. Once m is raised
+    // every P of later blocks stays below 2^TAU unless a new larger score
+    // arrives, which the same test catches.
+    // The basic block of each half (closed by that branch) holds its 8 MFMAs
+    // and the softmax's fast path; HALF (1 or 2) lays them out: in H1 the 12
+    // operand reads first, then softmax VALU work while they land, then one
+    // MFMA per 5 VALU instructions; in H2 (operands in registers) one MFMA per
+    // 6 from the start.
+    auto softmax_spec = [&](auto half_tag, const floatx16& sc, float& m, float& l, floatx16 (&o)[DB],
+                            half8 (&p)[2]) {
+        constexpr int HALF = decltype(half_tag)::value;
+        float ls = exps(sc, m, p);
+        if constexpr (HALF == 1) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);   // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);   // VALU
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // VALU
+            }
+        } else if constexpr (HALF == 2) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
+        }
+        if (__any(!(ls <= 256.0f))) {   // 2^TAU; also true for inf / NaN
+            raise(block_max(sc), m, l, o);
+            ls = exps(sc, m, p);
+        }
+        l += ls;
+    };
+
+    floatx16 oa[DB], ob[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) { oa[db] = floatx16{}; ob[db] = floatx16{}; }
+    float ma = -INFINITY, mb = -INFINITY, la = 0.f, lb = 0.f;
+    floatx16 sa, sb;
+    half8 pa[2], pb[2];
+    half8 kr[KS];
+    half8 vr[2][DB];
+
+    // Full blocks of this group run through the pipelined loop; the partial
+    // last block of the KV range (only the last group can hold it) is computed
+    // on its own after them, so the loop body needs no position checks.
+    const bool part = ng > 0 && (bs + ng) * BK > a.nkv;
+    const int nf = ng - (part ? 1 : 0);
+
+    // ---- prologue: blocks 0 and 1 landed; Q operands; S_A(0), S_B(0), P_A(0) ----
+    wait_blocks<NLD>(max(npre - 2, 0));
+    __syncthreads();   // Q staged, blocks 0 and 1 visible
+    half8 qa[KS], qb[KS];
+    {
+        const char* qs = smem + RING;
+        const int ra = 64 * wq + nl, rb = ra + 32;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            qa[ks] = *(const half8*)(qs + ra * ROW + (((2 * ks + hh) ^ (ra & 7)) * 16));
+            qb[ks] = *(const half8*)(qs + rb * ROW + (((2 * ks + hh) ^ (rb & 7)) * 16));
+        }
+    }
+    if (nf > 0) {
+        read_k(0, kr);
+        s_mfma(sa, qa, kr);
+        s_mfma(sb, qb, kr);
+        softmax_exact(sa, ma, la, oa, pa);
+        // the loop's softmax needs a finite running max to start from
+        mb = block_max(sb);
+    }
+
+    // ---- main loop: full blocks 0 .. nf - 2 ------------------------------------
+    // At the start of iteration t block t + 7 goes into slot (t - 1) % 8
+    // (block t - 1 was last read in iteration t - 1, before its barrier); at
+    // its end block t + 2 must have landed (read at the top of iteration t + 1).
+    // Every wavefront passes one barrier per block of the longest group (ni),
+    // plus the prologue's and the merge's.
+    for (int t = 0; t + 1 < nf; ++t) {
+        if (t + AHEAD < ng) issue(t + AHEAD);
+        read_k(t + 1, kr);
+        read_v(t, vr);
+        // H1: S_A(t+1), PV_A(t) on the matrix pipe; softmax of S_B(t). The
+        // MFMAs come first in the source so they share a basic block with
+        // the softmax's fast path (its rare rescale branch closes the block)
+        // and the scheduler can interleave the two.
+        s_mfma(sa, qa, kr);
+        pv_mfma(oa, pa, vr);
+        softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb);
+        // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
+        pv_mfma(ob, pb, vr);
+        s_mfma(sb, qb, kr);
+        softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa);
+        // loads of blocks t + 3 .. min(t + 7, ng - 1) may stay in flight
+        wait_blocks<NLD>(max(min(t + AHEAD, ng - 1) - (t + 2), 0));
+        __syncthreads();
+    }
+    // (no loads are issued from here on)
+    if (nf > 0) {
+        // last full block: PV_A, softmax of S_B, PV_B
+        read_v(nf - 1, vr);
+        pv_mfma(oa, pa, vr);
+        softmax_exact(sb, mb, lb, ob, pb);
+        pv_mfma(ob, pb, vr);
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
+    if (part) {
+        // the partial block, unpipelined
+        const int tp = nf;
+        read_k(tp, kr);
+        s_mfma(sa, qa, kr);
+        s_mfma(sb, qb, kr);
+        read_v(tp, vr);
+        tail_fix(sa, tp);
+        tail_fix(sb, tp);
+        softmax_exact(sa, ma, la, oa, pa);
+        softmax_exact(sb, mb, lb, ob, pb);
+        pv_mfma(oa, pa, vr);
+        pv_mfma(ob, pb, vr);
+        __syncthreads();
+    }
+    for (int tt = ng; tt < ni; ++tt) __syncthreads();
+
+    // ---- merge the KV groups through LDS (the ring is free), normalise ------------
+    // Groups 1.. publish (O, m, l) element-major (each wavefront's 64 lanes
+    // write consecutive words); group 0 merges and writes the normalised rows
+    // to a staging tile, row r at r * 256 bytes with 16-byte chunk j at
+    // position j ^ (r & 15); then all wavefronts store full rows.
+    constexpr int PUB = SH::PUB;
+    float* xs = (float*)smem;
+    char* ost = smem + SH::OST;
+    if (kg > 0) {
+        float* w = xs + ((kg - 1) * NQT + wq) * PUB * 64 + lane;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                w[(db * 16 + j) * 64] = oa[db][j];
+                w[(32 + db * 16 + j) * 64] = ob[db][j];
+            }
+        w[64 * 64] = ma;
+        w[65 * 64] = mb;
+        w[66 * 64] = la;
+        w[67 * 64] = lb;
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const float m = x ? mb : ma;
+            const float l = x ? lb : la;
+            const floatx16 (&o)[DB] = x ? ob : oa;
+            float M = m;
+#pragma unroll
+            for (int g = 1; g < KVG; ++g) M = fmaxf(M, xs[((g - 1) * NQT + wq) * PUB * 64 + (64 + x) * 64 + lane]);
+            const float Ms = (M == -INFINITY) ? 0.f : M;
+            const float w0 = exp2_fast(m - Ms);
+            float wg[KVG > 1 ? KVG - 1 : 1];
+            float lsum = l * w0;
+#pragma unroll
+            for (int g = 1; g < KVG; ++g) {
+                const float* r = xs + ((g - 1) * NQT + wq) * PUB * 64 + lane;
+                wg[g - 1] = exp2_fast(r[(64 + x) * 64] - Ms);
+                lsum = fmaf(wg[g - 1], r[(66 + x) * 64], lsum);
+            }
+            const float lt = pair32_sum(lsum);
+            const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
+            const float f0 = w0 * inv;
+#pragma unroll
+            for (int g = 1; g < KVG; ++g) wg[g - 1] *= inv;
+            const int row = 64 * wq + 32 * x + nl;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    floatx4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float acc = o[db][4 * a4 + e] * f0;
+#pragma unroll
+                        for (int g = 1; g < KVG; ++g)
+                            acc = fmaf(wg[g - 1], xs[((g - 1) * NQT + wq) * PUB * 64 + (32 * x + db * 16 + 4 * a4 + e) * 64 + lane], acc);
+                        v[e] = acc;
+                    }
+                    const int ch = 8 * db + 2 * a4 + hh;   // dims 4 ch .. 4 ch + 3
+                    *(floatx4*)(ost + row * 256 + ((ch ^ (row & 15)) * 16)) = v;
+                }
+        }
+    }
+    __syncthreads();
+    // ---- store: dst[b][row][h][0..63], 16 threads per 256-byte row -------------
+#pragma unroll
+    for (int u = 0; u < BM * 16 / NT; ++u) {
+        const int i = tid + NT * u;
+        const int r = i >> 4, ch = i & 15;
+        const int row = qw0 + r;
+        if (row < a.nq) {
+            const floatx4 v = *(const floatx4*)(ost + r * 256 + ((ch ^ (r & 15)) * 16));
+            *(floatx4*)(a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 4 * ch) = v;
+        }
+    }
+}
+
+template <class SH>
+static hipError_t launch_pp_shape(const AttnArgs& a, hipStream_t st) {
+    using namespace pp;
+    const int nqg = (a.nq + SH::BM - 1) / SH::BM;
+    const int nblk = (a.nkv + BK - 1) / BK;
+    const int ni = (nblk + SH::KVG - 1) / SH::KVG;
+    const int64_t nwg = (int64_t)nqg * a.hq * a.b;
+    if (nwg <= 0 || nwg > 0x7fffffff || nblk <= 0) return hipErrorInvalidValue;
+    // |scale| * log2(e) equal, bit for bit, to the literal in the kernel
+    const float c8 = 0.125f * kLog2e;
+    const bool is_c8 = fabsf(a.scale_log2) == c8 && __builtin_bit_cast(uint32_t, c8) == 0x3e38aa3bu;
+    const dim3 grid((unsigned)nwg), block(SH::NT);
+    if (a.q_f16) {
+        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<SH, true, true>), grid, block, 0, st, a, nqg, nblk, ni);
+        else hipLaunchKernelGGL((fa_prefill64_pp<SH, true, false>), grid, block, 0, st, a, nqg, nblk, ni);
+    } else {
+        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<SH, false, true>), grid, block, 0, st, a, nqg, nblk, ni);
+        else hipLaunchKernelGGL((fa_prefill64_pp<SH, false, false>), grid, block, 0, st, a, nqg, nblk, ni);
+    }
+    return hipGetLastError();
+}
+
+// hd 64 without a mask. shape 1: one wavefront per SIMD (128 query rows x 2
+// KV groups); shape 2: two per SIMD (128 query rows x 4 KV groups).
+hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t st) {
+    if (shape == 1) return launch_pp_shape<pp::Shape1>(a, st);
+    return launch_pp_shape<pp::Shape2>(a, st);
+}
+
+}  // namespace vxfa

@@ -28,6 +28,10 @@ struct vxfa_ctx {
     // VXFA_PREFILL_WAVES), read once when the context is created; 0 = heuristic
     int split_override = 0;
     int waves_override = 0;
+    // VXFA_PREFILL_PP=0 routes hd 64 unmasked prefill to the general kernel;
+    // VXFA_PP_SHAPE picks its workgroup shape (1 or 2, 0 = default)
+    bool pp_enabled = true;
+    int pp_shape = 0;
 };
 
 namespace {
@@ -147,6 +151,8 @@ vxfa_ctx* vxfa_ctx_create(int device) {
     c->device = device;
     if (const char* e = getenv("VXFA_DECODE_SPLIT")) c->split_override = atoi(e);
     if (const char* e = getenv("VXFA_PREFILL_WAVES")) c->waves_override = atoi(e);
+    if (const char* e = getenv("VXFA_PREFILL_PP")) c->pp_enabled = atoi(e) != 0;
+    if (const char* e = getenv("VXFA_PP_SHAPE")) c->pp_shape = atoi(e);
     return c;
 }
 
@@ -254,6 +260,11 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
             a.ws = c->ws;
         }
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
+    } else if (D == 64 && !mask && scale != 0.0f && c->pp_enabled) {
+        // (scale 0 goes to the general kernel: the pipelined one folds the
+        // scale into the exponent and scores the partial block's dead rows -inf)
+        // encoder prefill: the software-pipelined hd 64 kernel
+        e = vxfa::launch_prefill64_pp(a, c->pp_shape, st);
     } else {
         // query-row wavefronts per workgroup (each with its KV partner
         // wavefronts): 4 shares every staged K/V step among 128 query rows;
