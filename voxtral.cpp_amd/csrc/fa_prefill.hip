@@ -63,6 +63,104 @@ namespace vxfa {
 constexpr int PF_BN = 64;                // KV positions per wavefront tile
 constexpr float PF_TAU = 8.0f;
 
+constexpr int PF_MAXT = 512;            // 64-position tiles classified per row group
+
+// Tile classes of an additive mask over the workgroup's rows, for row group g
+// (32 rows) and 64-position tile T: flags[g * PF_MAXT + T] has bit 0 set when
+// some entry is not -inf and bit 1 when some entry is not +-0. So 1 = every
+// entry is zero (the tile needs no mask values), 2 = every entry is -inf (the
+// tile contributes nothing), 3 = mixed; a partial last tile with a live entry
+// counts as mixed, and a group without rows reads 0 (nothing to do). Tiles
+// from PF_MAXT on are not classified (read as mixed).
+// Also returns the live range [lo, hi) rounded out to whole tiles, which
+// selects the same KV steps as the exact range (steps are whole tiles).
+//
+// One wavefront takes one (group, tile) unit at a time, four units per
+// batch, all of a batch's loads issued before any is used. A unit's rows are
+// 128-byte segments at any 2-byte alignment (voxtral's n x n mask rows are 2n
+// bytes apart): nine lanes read one row's segment as the 16-byte-aligned
+// chunks that cover it, seven rows per load instruction, five instructions
+// per unit. Each chunk holds at least one byte of the row, so it lies in the
+// same 16-byte granule of the same allocation and page as mask data; entries
+// outside the segment are dropped in registers.
+template <int NT, int NG>
+__device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t row_stride, int rows, int n,
+                                                uint8_t* flags, int* red, int& lo, int& hi) {
+    constexpr int NWV = NT / 64;
+    constexpr int UB = 4;            // units per wavefront batch
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int ntile_all = (n + 63) >> 6;
+    const int ntile = min(ntile_all, PF_MAXT);
+    const int units = NG * ntile;
+    const int lr = lane / 9, lc = lane - 9 * lr;   // row in a batch of 7 (lane 63 idle), chunk 0..8
+    int tlo = 0x7fffffff, thi = -1;                // live tiles (wave-uniform)
+    for (int ub = wave * UB; ub < units; ub += NWV * UB) {
+        u32x4 w[UB][5];
+        int colc[UB][5];   // column of the chunk's first entry relative to the tile (may be < 0)
+#pragma unroll
+        for (int i = 0; i < UB; ++i) {
+            const int u = ub + i;
+            const int g = u / ntile, t = u - g * ntile;
+            const int c0 = 64 * t, c1 = min(64 * t + 64, n);
+#pragma unroll
+            for (int bt = 0; bt < 5; ++bt) {
+                const int rr = 7 * bt + lr;
+                const int row = 32 * g + rr;
+                const char* rowp = reinterpret_cast<const char*>(base) + (int64_t)row * row_stride;
+                const char* s0p = rowp + 2 * c0;
+                const int mis = (int)(reinterpret_cast<uintptr_t>(s0p) & 15);
+                const int off = 16 * lc - mis;               // chunk start relative to s0p, bytes
+                const bool ok = u < units && lr < 7 && rr < 32 && row < rows && off < 2 * (c1 - c0);
+                colc[i][bt] = ok ? off / 2 : 64;             // 64: no entry in the tile
+                w[i][bt] = u32x4{0u, 0u, 0u, 0u};
+                if (ok) w[i][bt] = *reinterpret_cast<const u32x4*>(s0p + off);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < UB; ++i) {
+            const int u = ub + i;
+            if (u >= units) break;
+            const int g = u / ntile, t = u - g * ntile;
+            const int span = min(64 * t + 64, n) - 64 * t;
+            uint32_t acc_l = 0, acc_n = 0;
+#pragma unroll
+            for (int bt = 0; bt < 5; ++bt) {
+                // entries [e_lo, e_hi) of the chunk lie in the tile's span
+                const int e_lo = min(max(-colc[i][bt], 0), 8);
+                const int e_hi = min(max(span - colc[i][bt], 0), 8);
+                const uint32_t m8 = e_hi > e_lo ? ((1u << (e_hi - e_lo)) - 1u) << e_lo : 0u;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t s0 = (uint32_t)(((int32_t)(m8 << (31 - 2 * j))) >> 31);
+                    const uint32_t s1 = (uint32_t)(((int32_t)(m8 << (30 - 2 * j))) >> 31);
+                    const uint32_t hm = (s0 & 0xFFFFu) | (s1 & 0xFFFF0000u);
+                    acc_l |= (w[i][bt][j] ^ 0xFC00FC00u) & hm;   // a half is not -inf
+                    acc_n |= (w[i][bt][j] & 0x7FFF7FFFu) & hm;   // a half is not +-0
+                }
+            }
+            const bool live = __any(acc_l != 0);
+            const bool nonzero = __any(acc_n != 0);
+            uint32_t bits = (live ? 1u : 0u) | (nonzero ? 2u : 0u);
+            if (live && span < 64) bits = 3u;
+            if (live) { tlo = min(tlo, t); thi = max(thi, t); }
+            if (lane == 0) flags[g * PF_MAXT + t] = (uint8_t)bits;
+        }
+    }
+    if (lane == 0) { red[2 * wave] = tlo; red[2 * wave + 1] = thi; }
+    __syncthreads();
+    tlo = red[0];
+    thi = red[1];
+#pragma unroll
+    for (int wv = 1; wv < NWV; ++wv) { tlo = min(tlo, red[2 * wv]); thi = max(thi, red[2 * wv + 1]); }
+    __syncthreads();   // red may be reused by the caller
+    if (ntile_all > PF_MAXT) {   // unclassified tail: keep it in the range
+        tlo = min(tlo, PF_MAXT);
+        thi = ntile_all - 1;
+    }
+    if (thi < 0) { lo = 0; hi = 0; } else { lo = 64 * tlo; hi = min(64 * thi + 64, n); }
+}
+
 template <int D, int NQW, int KVG, bool MASK, bool QF16>
 __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, int nqt) {
     static_assert(D == 64 || D == 128, "head dim");
@@ -86,6 +184,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     __shared__ __attribute__((aligned(16))) char sK[2 * TILE_BYTES];
     __shared__ float s_ml[KVG > 1 ? 2 * (KVG - 1) * NQW * 64 : 1];
     __shared__ int s_red[2 * NW];
+    __shared__ uint8_t s_tflag[MASK ? NQW * PF_MAXT : 1];
 
     // ---- XCD-aware position of this workgroup --------------------------------
     const int nwg = gridDim.x;
@@ -113,9 +212,28 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     const bool qvalid = qrow < a.nq;
     const int nstep = (a.nkv + BS - 1) / BS;         // BS-position steps
 
-    // ---- live column range of the mask over this workgroup's rows -----------
-    // Steps wholly outside the range are never loaded; a tile inside it whose
-    // mask entries are all -inf is skipped after its load (tile()).
+    // ---- Q operand (B of S^T = K Q^T): row qrow, dims 16ks + 8hh .. +7 ----
+    // (the Q element type is a template parameter: a load-or-convert branch on
+    // it makes the compiler wait for all global loads inside the KV loop).
+    // Rows past n_q load row 0 and are zeroed, so all loads issue back to back
+    // (before the mask scan, whose loads then share their round trip).
+    half8 qb[KS];
+    {
+        constexpr int qelt = QF16 ? 2 : 4;
+        const int64_t qoff = (int64_t)(qvalid ? qrow : 0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 v = load_q8(a.q, qoff + (int64_t)(16 * ks + 8 * hh) * qelt, QF16);
+            qb[ks] = qvalid ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
+
+    // ---- live column range and tile classes of the mask over this workgroup's
+    // rows ----------------------------------------------------------------------
+    // Steps wholly outside the range are never loaded. Inside it, a wavefront's
+    // tile whose entries are all -inf is skipped, one whose entries are all
+    // zero is computed without reading the mask, and only mixed tiles (the
+    // diagonal of a causal mask, the edges of a window) read mask values.
     const uint16_t* mplane = nullptr;
     int step_lo = 0, step_hi = nstep;
     if (MASK) {
@@ -123,8 +241,8 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
                                    (int64_t)(b % a.bm) * a.m_nb3);
         int lo = 0, hi = 0;
         const int rows = min(BM, a.nq - q0);
-        mask_live_range<NT>((const uint16_t*)((const char*)mplane + (int64_t)q0 * a.m_nb1), a.m_nb1, rows, a.nkv,
-                            s_red, lo, hi);
+        mask_scan_tiles<NT, NQW>((const uint16_t*)((const char*)mplane + (int64_t)q0 * a.m_nb1), a.m_nb1, rows,
+                                 a.nkv, s_tflag, s_red, lo, hi);
         step_lo = lo / BS;
         step_hi = hi > lo ? (hi - 1) / BS + 1 : 0;
     }
@@ -144,20 +262,6 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     int first = -1;
     if (!MASK) first = nstep == 1 ? 0 : (int)(((int64_t)qt * (nstep - 1)) / nqt);
     else if (step_lo < step_hi) first = step_lo;
-
-    // ---- Q operand (B of S^T = K Q^T): row qrow, dims 16ks + 8hh .. +7 ----
-    // (the Q element type is a template parameter: a load-or-convert branch on
-    // it makes the compiler wait for all global loads inside the KV loop)
-    half8 qb[KS];
-    {
-        constexpr int qelt = QF16 ? 2 : 4;
-        const int64_t qoff = (int64_t)(qvalid ? qrow : 0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            if (qvalid) qb[ks] = load_q8(a.q, qoff + (int64_t)(16 * ks + 8 * hh) * qelt, QF16);
-            else qb[ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-    }
 
     // ---- step loads: global -> LDS ------------------------------------------
     // Instruction i of wavefront w fills rows [ROWS_PER_LOAD * (w + NW i), + ROWS_PER_LOAD)
@@ -279,9 +383,13 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
 
     // One 64-position tile at kv0 from LDS stage stg.
     // TAIL: the tile runs past n_kv (positions >= n_kv are forced to -inf).
-    auto tile = [&](auto tail_tag, int stg, int kv0, const uint32_t (&mw)[2][8]) {
-        constexpr bool TAIL = !MASK && decltype(tail_tag)::value;   // the mask path covers the tail
-        if constexpr (MASK) {
+    // M: add the mask words mw (a mixed tile); without M the tile is computed
+    // as unmasked (no mask, or a tile whose mask entries are all zero, which
+    // never runs past n_kv: entries there read as -inf).
+    auto tile = [&](auto tail_tag, auto mask_tag, int stg, int kv0, const uint32_t (&mw)[2][8]) {
+        constexpr bool M = decltype(mask_tag)::value;
+        constexpr bool TAIL = !M && decltype(tail_tag)::value;   // the mask path covers the tail
+        if constexpr (M) {
             bool any = false;
 #pragma unroll
             for (int kvb = 0; kvb < 2; ++kvb)
@@ -308,14 +416,14 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         // max (max(c*s) = c*max(s) for c >= 0, c*min(s) for c < 0) and folded
         // into the exp2 argument, one FMA per score.
         float mx;
-        if (MASK || TAIL) {
+        if (M || TAIL) {
             mx = -INFINITY;
 #pragma unroll
             for (int kvb = 0; kvb < 2; ++kvb)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     float x = S[kvb][j] * c;
-                    if constexpr (MASK) {
+                    if constexpr (M) {
                         const half2 m2 = __builtin_bit_cast(half2, mw[kvb][j >> 1]);
                         x = fmaf((float)m2[j & 1], kLog2e, x);   // -inf stays -inf
                     }
@@ -360,7 +468,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
             half8 pb;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float e = (MASK || TAIL) ? S[kvb][8 * cc + i] - msafe : fmaf(S[kvb][8 * cc + i], c, -msafe);
+                const float e = (M || TAIL) ? S[kvb][8 * cc + i] - msafe : fmaf(S[kvb][8 * cc + i], c, -msafe);
                 pb[i] = (_Float16)exp2_fast(e);
             }
 #pragma unroll
@@ -386,15 +494,30 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // every wavefront. The stage is a template constant so every LDS read
     // address is a register plus an immediate.
     uint32_t mwa[2][8], mwb[2][8];
+    // class of this wavefront's tile at kv0 (MASK only): 1 all zero, 2 or 0
+    // dead, 3 mixed
+    auto tclass = [&](int kv0) -> int {
+        const int t = kv0 / PF_BN;
+        return t < PF_MAXT ? (int)s_tflag[qw * PF_MAXT + t] : 3;
+    };
+    auto run_tile = [&](int stg, int kv0, const uint32_t (&mw)[2][8]) {
+        if constexpr (MASK) {
+            const int f = tclass(kv0);
+            if (f == 3) tile(std::false_type{}, std::true_type{}, stg, kv0, mw);
+            else if (f == 1) tile(std::false_type{}, std::false_type{}, stg, kv0, mw);
+        } else {
+            tile(std::false_type{}, std::false_type{}, stg, kv0, mw);
+        }
+    };
     auto run_step = [&](auto stg_tag, int s_cur, int s_nxt, const uint32_t (&mw_cur)[2][8], uint32_t (&mw_nxt)[2][8]) {
         constexpr int STG = decltype(stg_tag)::value;
         if (s_nxt >= 0) {
             issue_step(s_nxt, STG ^ 1);
             const int kv0n = s_nxt * BS + PF_BN * kg;
-            if (MASK && kv0n < a.nkv) load_mask(kv0n, mw_nxt);
+            if (MASK && kv0n < a.nkv && tclass(kv0n) == 3) load_mask(kv0n, mw_nxt);
         }
         const int kv0 = s_cur * BS + PF_BN * kg;
-        if (kv0 < a.nkv) tile(std::false_type{}, STG, kv0, mw_cur);
+        if (kv0 < a.nkv) run_tile(STG, kv0, mw_cur);
         wait_all_mem();
         __syncthreads();
     };
@@ -406,7 +529,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     if (s_cur >= 0) {
         issue_step(s_cur, 0);
         const int kv0 = s_cur * BS + PF_BN * kg;
-        if (MASK && kv0 < a.nkv) load_mask(kv0, mwa);
+        if (MASK && kv0 < a.nkv && tclass(kv0) == 3) load_mask(kv0, mwa);
     }
     wait_all_mem();
     __syncthreads();
@@ -423,7 +546,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     }
     if (!MASK && s_cur >= 0) {
         const int kv0 = s_cur * BS + PF_BN * kg;
-        if (kv0 < a.nkv) tile(std::true_type{}, last_stage, kv0, mwa);   // mask words unused
+        if (kv0 < a.nkv) tile(std::true_type{}, std::false_type{}, last_stage, kv0, mwa);   // mask words unused
         __syncthreads();
     }
 
