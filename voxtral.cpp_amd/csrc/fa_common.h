@@ -243,6 +243,10 @@ __device__ __forceinline__ float pair32_sum(float x) {
 namespace vxfa {
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t stream);
 constexpr int kDecodeMaxSplit = 64;
+constexpr int kDecodeWaves = 4;      // wavefronts per decode split workgroup
+// Floats per decode partial record: O [G][D], then m [G] and l [G], padded to
+// a multiple of 4 so every record starts 16-byte aligned.
+constexpr int dec_record_floats(int D, int G) { return G * D + ((2 * G + 3) & ~3); }
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
 hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);

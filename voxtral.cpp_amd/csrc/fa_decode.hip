@@ -7,16 +7,21 @@
 // serves G = Hq / Hkv query heads (32 / 8 = 4).
 //
 // Two kernels on the caller's stream:
-//   fa_decode_split   grid (n_split, Hkv, B), 4 wavefronts per workgroup.
-//                     Each workgroup reduces one contiguous slice of the live
-//                     KV range to (O, m, l) per query head of its group.
-//   fa_decode_combine grid (Hkv * G, B): log-sum-exp merge of the n_split
-//                     partials of one query head, in a fixed order
-//                     (deterministic output).
+//   fa_decode_split   grid (n_split * Hkv, B), kDecodeWaves wavefronts per
+//                     workgroup, the kv head fastest-varying (neighbouring
+//                     workgroups stream neighbouring 256-byte head slices of
+//                     the same cache rows). Each workgroup reduces one
+//                     contiguous slice of the live KV range to (O, m, l) per
+//                     query head of its group.
+//   fa_decode_combine grid (Hq * D / 32, B), one wavefront per (query head,
+//                     32 output dims): log-sum-exp merge of the n_split
+//                     partials in a fixed order (deterministic output).
 // With n_split == 1 the split kernel writes the output and no merge runs.
-// The kernel boundary orders the partials' stores before the merge's loads;
-// an in-kernel last-block merge needs an agent-scope release fence (an L2
-// write-back per workgroup), which measured slower than the second launch.
+// The kernel boundary orders the partials' stores before the merge's loads.
+// A merge inside the split kernel by the last workgroup to finish (device-
+// scope stores, an arrival counter, an acquire fence) measured slower: the
+// counter's round trip plus one CU reading all n_split records (its load
+// parallelism caps it near 20-30 GB/s) cost more than the kernel boundary.
 //
 // Inside a wavefront (32-position tiles, software pipelined: the next tile's
 // K/V loads are in flight while the current tile is computed):
@@ -39,7 +44,7 @@
 
 namespace vxfa {
 
-constexpr int DEC_WAVES = 4;
+constexpr int DEC_WAVES = kDecodeWaves;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 constexpr int DEC_TILE = 32;
 
@@ -57,13 +62,14 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     __shared__ float lds_m[DEC_WAVES][G];
     __shared__ float lds_l[DEC_WAVES][G];
     __shared__ int lds_red[2 * DEC_WAVES];
+    __shared__ half8 lds_q[G * D / 8];   // the group's query heads, f16, [G][D]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int split = blockIdx.x;
-    const int g = blockIdx.y;
-    const int b = blockIdx.z;
+    const int g = blockIdx.x % a.hkv;
+    const int split = blockIdx.x / a.hkv;
+    const int b = blockIdx.y;
     const int bkv = b / (a.b / a.bk);
     constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
 
@@ -139,33 +145,48 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     };
 
     // ---- prologue: Q and the first tile go out together -------------------
-    // (the Q element type is a template parameter: a load-or-convert branch on
-    // it makes the compiler wait for all global loads inside the KV loop)
-    const int hq_lane = g * G + ((lane & 15) % G);  // A-operand row m = lane & 15 -> head m % G
-    const int64_t qoff = (int64_t)hq_lane * a.q_nb2 + (int64_t)b * a.q_nb3;
+    // The group's G query heads (G * D elements, contiguous per head) are read
+    // once per workgroup, 8 elements per thread, rounded to f16 (ggml's Q
+    // conversion before an f16 K dot product) and staged in LDS; each
+    // wavefront then reads its MFMA A operand (head (lane & 15) % G, dims
+    // 32 ks + 8 (lane >> 4) .. + 7) from there. (The Q element type is a
+    // template parameter: a load-or-convert branch on it makes the compiler
+    // wait for all global loads inside the KV loop.)
     constexpr int QCH = QF16 ? 1 : 2;                // 16-byte loads per 8 elements
-    floatx4 qraw[KS][QCH];
+    constexpr int QTHREADS = G * D / 8;              // threads holding 8 Q elements
+    static_assert(QTHREADS <= DEC_THREADS, "Q staging");
+    floatx4 qraw[QCH];
+    const bool q_loader = tid < QTHREADS;
+    {
+        const int qh = g * G + (q_loader ? tid / (D / 8) : 0);
+        const int qd = q_loader ? 8 * (tid % (D / 8)) : 0;
+        const floatx4* p = (const floatx4*)((const char*)a.q + (int64_t)qh * a.q_nb2 + (int64_t)b * a.q_nb3 +
+                                            (int64_t)qd * (QF16 ? 2 : 4));
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const floatx4* p = (const floatx4*)((const char*)a.q + qoff + (int64_t)(32 * ks + 8 * (lane >> 4)) * (QF16 ? 2 : 4));
-#pragma unroll
-        for (int u = 0; u < QCH; ++u) qraw[ks][u] = p[u];
+        for (int u = 0; u < QCH; ++u) qraw[u] = p[u];
     }
     Tile TA, TB;
     int t = t_begin + wave;
     if (t < t_end) load_tile(TA, t);
-    half8 qa[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    if (q_loader) {
+        half8 qh8;
         if constexpr (QF16) {
-            qa[ks] = __builtin_bit_cast(half8, qraw[ks][0]);
+            qh8 = __builtin_bit_cast(half8, qraw[0]);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                qa[ks][e] = (_Float16)qraw[ks][0][e];
-                qa[ks][4 + e] = (_Float16)qraw[ks][QCH - 1][e];
+                qh8[e] = (_Float16)qraw[0][e];
+                qh8[4 + e] = (_Float16)qraw[QCH - 1][e];
             }
         }
+        lds_q[tid] = qh8;
+    }
+    __syncthreads();
+    half8 qa[KS];
+    {
+        const int m = (lane & 15) % G;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qa[ks] = lds_q[(m * D + 32 * ks + 8 * (lane >> 4)) / 8];
     }
 
     float m_run[4], l_run[4];
@@ -275,7 +296,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
 
     float* rec = nullptr;
     if (a.n_split > 1)
-        rec = a.ws + ((int64_t)(b * a.hkv + g) * a.n_split + split) * (G * (D + 2));
+        rec = a.ws + ((int64_t)(b * a.hkv + g) * a.n_split + split) * dec_record_floats(D, G);
     for (int o = tid; o < G * D; o += DEC_THREADS) {
         const int h = o / D, d = o % D;
         float M = lds_m[0][h];
@@ -298,82 +319,75 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     }
 }
 
-// Log-sum-exp merge of the n_split partial records of one query head:
+// Log-sum-exp merge of the n_split partial records, one wavefront per
+// (query head, 32 output dims):
 //   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
-// Grid (Hkv * G, B): one workgroup per query head. The O partials are loaded
-// first (their addresses do not depend on the weights), then wavefront 0
-// loads the n_split (m, l) pairs, one per lane, and forms the weights with
-// wavefront reductions; the whole merge costs one memory round trip. The
-// summation order is fixed, so the output is deterministic.
+// Lane (f, grp) loads float4 f of the slice from splits grp, grp + 8, ...
+// while lane s loads split s's (m, l); all loads issue back to back (loads
+// past the last split read the last record again; their weights are zero), so
+// the merge costs one memory round trip. Wavefront reductions form the
+// weights and the sums, in a fixed order: the output is deterministic.
 template <int D, int G>
-__global__ __launch_bounds__(DEC_THREADS) void fa_decode_combine(AttnArgs a) {
-    constexpr int NF4 = D / 4;                    // float4 per head row
-    constexpr int NGRP = DEC_THREADS / NF4;       // split groups
-    constexpr int MAXS = kDecodeMaxSplit / NGRP;  // splits per thread
-    static_assert(NGRP * NF4 == DEC_THREADS && MAXS * NGRP == kDecodeMaxSplit, "combine split");
-    static_assert(kDecodeMaxSplit == 64, "one (m, l) pair per lane of wavefront 0");
-    __shared__ float cw[kDecodeMaxSplit];
-    __shared__ float cL;
-    __shared__ floatx4 cpart[NGRP][NF4];
-
-    const int tid = threadIdx.x;
-    const int g = blockIdx.x / G, h = blockIdx.x % G;
+__global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
+    constexpr int CSUB = D / 32;                  // 32-dim slices per head
+    constexpr int CF4 = 8;                        // float4 per slice
+    constexpr int NGRP = 64 / CF4;                // split groups
+    constexpr int MAXS = kDecodeMaxSplit / NGRP;  // splits per lane
+    constexpr int RS = dec_record_floats(D, G);
+    static_assert(kDecodeMaxSplit == 64, "one (m, l) pair per lane");
+    const int lane = threadIdx.x;
+    const int hq = blockIdx.x / CSUB, sl = blockIdx.x % CSUB;
+    const int g = hq / G, h = hq % G;
     const int b = blockIdx.y;
-    const int rs = G * (D + 2);
     const int ns = a.n_split;
-    const float* base = a.ws + (int64_t)(b * a.hkv + g) * ns * rs;
-    const int f = tid % NF4, grp = tid / NF4;
+    const float* base = a.ws + (int64_t)(b * a.hkv + g) * ns * RS;
+    const int f = lane % CF4, grp = lane / CF4;
 
     floatx4 o[MAXS];
 #pragma unroll
     for (int i = 0; i < MAXS; ++i) {
-        const int sp = grp + i * NGRP;
-        o[i] = sp < ns ? *(const floatx4*)(base + (int64_t)sp * rs + h * D + 4 * f) : floatx4{0.f, 0.f, 0.f, 0.f};
+        const int sp = min(grp + i * NGRP, ns - 1);
+        o[i] = *(const floatx4*)(base + (int64_t)sp * RS + h * D + 32 * sl + 4 * f);
     }
-    if (tid < 64) {
-        const float m = tid < ns ? base[(int64_t)tid * rs + G * D + h] : -INFINITY;
-        const float l = tid < ns ? base[(int64_t)tid * rs + G * D + G + h] : 0.f;
-        float M = m;
+    const float* r = base + (int64_t)min(lane, ns - 1) * RS + G * D;
+    float m = r[h], l = r[G + h];
+    m = lane < ns ? m : -INFINITY;
+    l = lane < ns ? l : 0.f;
+    float M = m;
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-        const float Ms = (M == -INFINITY) ? 0.f : M;
-        const float w = exp2_fast(m - Ms);        // 0 for an empty split (m = -inf)
-        float L = w * l;
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    const float w = exp2_fast(m - Ms);            // 0 for an empty split (m = -inf)
+    float L = w * l;
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
-        cw[tid] = w;
-        if (tid == 0) cL = L;
-    }
-    __syncthreads();
+    for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
+
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < MAXS; ++i) {
         const int sp = grp + i * NGRP;
-        const float w = sp < ns ? cw[sp] : 0.f;
-        acc[0] = fmaf(w, o[i][0], acc[0]);
-        acc[1] = fmaf(w, o[i][1], acc[1]);
-        acc[2] = fmaf(w, o[i][2], acc[2]);
-        acc[3] = fmaf(w, o[i][3], acc[3]);
+        const float ws = __shfl(w, sp & 63, 64);
+        const float wt = sp < ns ? ws : 0.f;
+        acc[0] = fmaf(wt, o[i][0], acc[0]);
+        acc[1] = fmaf(wt, o[i][1], acc[1]);
+        acc[2] = fmaf(wt, o[i][2], acc[2]);
+        acc[3] = fmaf(wt, o[i][3], acc[3]);
     }
-    cpart[grp][f] = acc;
-    __syncthreads();
-    if (tid < NF4) {
-        floatx4 s = cpart[0][tid];
 #pragma unroll
-        for (int p = 1; p < NGRP; ++p) {
-            const floatx4 y = cpart[p][tid];
-            s[0] += y[0]; s[1] += y[1]; s[2] += y[2]; s[3] += y[3];
-        }
-        const float L = cL;
+    for (int off = CF4; off < 64; off <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += shfl_xor(acc[c], off);
+    if (grp == 0) {
         const float inv = (L == 0.f) ? 0.f : 1.0f / L;
-        const floatx4 out = {s[0] * inv, s[1] * inv, s[2] * inv, s[3] * inv};
-        *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G + h) * D + 4 * tid) = out;
+        const floatx4 out = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        *(floatx4*)(a.dst + ((int64_t)b * a.hq + hq) * D + 32 * sl + 4 * f) = out;
     }
 }
 
 template <int D, int G>
 static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
-    const dim3 grid(a.n_split, a.hkv, a.b), block(DEC_THREADS);
+    if (a.b > 65535) return hipErrorInvalidValue;
+    const dim3 grid(a.n_split * a.hkv, a.b), block(DEC_THREADS);
     if (a.mask) {
         if (a.q_f16) hipLaunchKernelGGL((fa_decode_split<D, G, true, true>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((fa_decode_split<D, G, false, true>), grid, block, 0, st, a);
@@ -382,7 +396,7 @@ static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
         else hipLaunchKernelGGL((fa_decode_split<D, G, false, false>), grid, block, 0, st, a);
     }
     if (a.n_split > 1)
-        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G, a.b), dim3(DEC_THREADS), 0, st, a);
+        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G * (D / 32), a.b), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -126,13 +126,13 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
     return VXFA_OK;
 }
 
-// Workgroups per (batch, kv head) for the decode split kernel: enough to
-// cover the chip twice over (256 CUs), at least 128 positions per workgroup,
+// Workgroups per (batch, kv head) for the decode split kernel: 2048
+// wavefronts in all (8 per CU), at least one 32-position tile per wavefront,
 // and at most kDecodeMaxSplit so the merge stays short.
 int choose_split(int64_t pairs, int64_t nkv) {
-    const int64_t target = 512;
+    const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
-    const int64_t by_len = (nkv + 127) / 128;
+    const int64_t by_len = (nkv + 32 * vxfa::kDecodeWaves - 1) / (32 * vxfa::kDecodeWaves);
     if (s > by_len) s = by_len;
     if (s > 64) s = 64;
     if (s < 1) s = 1;
@@ -241,7 +241,7 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
         if (c->split_override > 0) S = c->split_override < vxfa::kDecodeMaxSplit ? c->split_override : vxfa::kDecodeMaxSplit;
         a.n_split = S;
         if (S > 1) {
-            const size_t need = (size_t)(B * Hkv) * S * G * (D + 2);
+            const size_t need = (size_t)(B * Hkv) * S * vxfa::dec_record_floats((int)D, (int)G);
             if (need > c->ws_floats) {
                 // grow: work queued earlier on this stream may still read the old buffer
                 if (c->ws) {
