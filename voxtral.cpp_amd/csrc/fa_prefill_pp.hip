@@ -1,25 +1,29 @@
 // fa_prefill_pp.hip — encoder self-attention prefill (hd 64, no mask) for
-// gfx950: one wavefront per SIMD, software-pipelined so the matrix pipe and
-// the VALU overlap inside the wavefront.
+// gfx950, software-pipelined so the matrix pipe and the VALU overlap inside
+// each wavefront.
 //
 // Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the offline
 // encoder call of voxtral.cpp: hd 64, 20 heads, 1500 frames, bidirectional,
 // mask = null, scale = 1/sqrt(64) (src/voxtral.cpp:1580-1613, FA at :1611).
 //
 // Work decomposition
-//   Workgroup = 2 query tiles of 64 rows x 2 KV groups = 4 wavefronts, one
-//   per SIMD. KV group g walks its own contiguous half of the 32-position
-//   blocks; the two groups' partial (O, m, l) are merged through LDS at the
-//   end. At 1500 x 20 the grid is 12 x 20 = 240 workgroups, one per CU. The
-//   workgroups of one head are dealt to one XCD (workgroups go to the 8 XCDs
-//   round robin), so that head's K/V stays in one L2.
+//   Workgroup = NQT query tiles of 64 rows x KVG KV groups, one wavefront
+//   each. KV group g walks its own contiguous share of the 32-position
+//   blocks; the groups' partial (O, m, l) are merged through LDS at the end.
+//   Two shapes: Shape1 = 2 x 2 (4 wavefronts, one per SIMD, 8-slot ring) and
+//   Shape2 = 2 x 4 (8 wavefronts, two per SIMD, 4-slot ring), the default:
+//   the second wavefront on a SIMD covers the first one's memory and
+//   dependency stalls (26.5 against 28.3 us per encoder layer). At 1500 x 20
+//   the grid is 12 x 20 = 240 workgroups, one per CU. The workgroups of one
+//   head are dealt to one XCD (workgroups go to the 8 XCDs round robin), so
+//   that head's K/V stays in one L2.
 // Why 64 query rows per wavefront: every K and V operand read from LDS feeds
 //   two MFMAs (one per 32-row half), half the LDS reads per FLOP of a 32-row
 //   wavefront, whose operand reads alone would need the full LDS bandwidth
 //   at the MFMA peak.
-// Why one wavefront per SIMD: all its state (O, Q, S, P, K and V operands of
-//   both halves, ~230 VGPRs) stays in registers with no copies, and there is
-//   no second wavefront on the SIMD for the issue arbiter to favour.
+// Register budget: all of a wavefront's state (O, Q, S, P, K and V operands
+//   of both halves, 200-230 VGPRs) stays in registers with no copies, which
+//   fits two wavefronts per SIMD (256 VGPRs each).
 // Ping-pong inside the wavefront: the halves A (rows 0-31) and B (rows 32-63)
 //   run half an iteration apart. Iteration t (block t of the group):
 //     H1: MFMA  O_A += V_t^T P_A(t)^T, S_A(t+1) = K_{t+1} Q_A^T
@@ -30,14 +34,14 @@
 //   scheduler interleaves them. K_{t+1} and V_t are read at the top of
 //   iteration t; the softmax of S_B(t) needs neither, so the VALU (the
 //   busier pipe for hd 64) can start while the reads land.
-// K/V staging: an 8-slot LDS ring; block b sits in slot b % 8, its K is read
-//   at the top of iteration b - 1 and its V at the top of iteration b; block
-//   b + 7 goes into the slot of block b - 1 at the start of iteration b, one
-//   barrier after that block's last read (global_load_lds_dwordx4, no
-//   staging registers). A block therefore has five iterations to arrive; at
-//   the end of iteration t each wavefront waits only for its own loads of
-//   block t + 2 (s_waitcnt vmcnt counting the younger blocks still in
-//   flight), then one barrier.
+// K/V staging: an NS-slot LDS ring; block b sits in slot b % NS, its K is
+//   read at the top of iteration b - 1 and its V at the top of iteration b;
+//   block b + NS - 1 goes into the slot of block b - 1 at the start of
+//   iteration b, one barrier after that block's last read
+//   (global_load_lds_dwordx4, no staging registers). A block therefore has
+//   NS - 3 iterations to arrive; at the end of iteration t each wavefront
+//   waits only for its own loads of block t + 2 (s_waitcnt vmcnt counting the
+//   younger blocks still in flight), then one barrier.
 // Q is loaded coalesced by the whole workgroup, rounded to f16 and staged in
 //   LDS; the output goes out through LDS as full 256-byte rows.
 // LDS rows and swizzles, MFMA operand layouts and the row-to-KV permutation
