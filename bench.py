@@ -67,10 +67,11 @@ def randn(torch, shape, seed, sigma=1.0, dtype=None):
 class Layer:
     """Descriptors of one flash_attn_ext call plus the tensors behind them."""
 
-    def __init__(self, q, k, v, mask, dst, scale, keep):
+    def __init__(self, q, k, v, mask, dst, scale, keep, md=None):
         self.q, self.k, self.v, self.mask, self.dst = q, k, v, mask, dst
         self.scale = scale
         self.keep = keep
+        self.md = md   # vxfa_mask_desc for the implicit-mask entry point, else None
 
 
 def f32s(x):
@@ -156,7 +157,10 @@ def time_calls(torch, ctx, calls, steps, warmup, graph=True):
 
     def one_step(sh):
         for L in calls:
-            ctx.flash_attn_ext(L.q, L.k, L.v, L.mask, L.dst, L.scale, stream=sh)
+            if L.md is not None:   # implicit causal / window mask
+                ctx.flash_attn_ext_implicit(L.q, L.k, L.v, L.md, L.dst, L.scale, stream=sh)
+            else:
+                ctx.flash_attn_ext(L.q, L.k, L.v, L.mask, L.dst, L.scale, stream=sh)
 
     with torch.cuda.stream(stream):
         for _ in range(max(1, warmup)):   # also sizes the workspace before capture
@@ -330,13 +334,21 @@ def main():
         configs["decoder_prefill_439_causal"] = {"us_per_layer": us, "tflops": tf,
                                                  "frac_mfma_peak": tf / MFMA_PEAK_TFLOPS,
                                                  "flops_per_layer": fl, "layers": 30}
+        # the same layers with the causal mask as a descriptor (no mask tensor)
+        md = vxfa.mask_desc(vxfa.MASK_CAUSAL, 0, 0)
+        impl = [Layer(L.q, L.k, L.v, None, L.dst, L.scale, L.keep, md) for L in pl]
+        _, us_i = time_calls(torch, ctx, impl, K, W)
+        tf_i = fl / (us_i * 1e-6) / 1e12
+        log(f"[decoder prefill 439 causal, implicit mask] {us_i:.2f} us/layer  {tf_i:.1f} TFLOP/s")
+        configs["decoder_prefill_439_causal"].update({"implicit_mask_us_per_layer": us_i, "implicit_mask_tflops": tf_i})
+        del impl
         del pl
         torch.cuda.empty_cache()
 
     if want("sliding"):
         cap, n0, window, steps = 16384, 16284, 2048, 100
         res = {}
-        for mode, ncache in (("cold", 8), ("warm", 1)):
+        for mode, ncache, implicit in (("cold", 8, False), ("warm", 1, False), ("implicit", 8, True)):
             caches = decode_layers(torch, ncache, cap, capacity=cap, seed=4000)
             masks = []
             calls = []
@@ -347,20 +359,22 @@ def main():
                 masks.append(m)
                 L = caches[t % ncache]
                 kne, knb = views.kv_cache(n_kv, 8, 128, cap)
+                md = vxfa.mask_desc(vxfa.MASK_CAUSAL, window, n_kv - 1) if implicit else None
+                mdesc = None if implicit else vxfa.desc(m.data_ptr(), vxfa.F16, *views.mask(n_kv, 1))
                 calls.append(Layer(L.q, vxfa.desc(L.k.data, vxfa.F16, kne, knb),
-                                   vxfa.desc(L.v.data, vxfa.F16, kne, knb),
-                                   vxfa.desc(m.data_ptr(), vxfa.F16, *views.mask(n_kv, 1)), L.dst, L.scale, None))
+                                   vxfa.desc(L.v.data, vxfa.F16, kne, knb), mdesc, L.dst, L.scale, None, md))
             _, us = time_calls(torch, ctx, calls, max(1, K // 4), 1)
-            by = decode_bytes(window, mask_bytes=2 * (n0 + steps // 2))
+            by = decode_bytes(window, mask_bytes=0 if implicit else 2 * (n0 + steps // 2))
             res[mode] = (us, by / (us * 1e-6) / 1e9)
             del caches, calls, masks
             torch.cuda.empty_cache()
         log(f"[sliding window] cold {res['cold'][0]:.2f} us/step {res['cold'][1]:.0f} GB/s; "
-            f"warm {res['warm'][0]:.2f} us/step")
+            f"warm {res['warm'][0]:.2f} us/step; implicit mask (cold) {res['implicit'][0]:.2f} us/step")
         configs["sliding_window_decode_16k_w2048"] = {
             "us_per_step_cold": res["cold"][0], "gbs_cold": res["cold"][1],
             "frac_hbm_peak_cold": res["cold"][1] / HBM_PEAK_GBS,
             "us_per_step_warm": res["warm"][0], "gbs_warm": res["warm"][1], "steps": steps,
+            "implicit_mask_us_per_step_cold": res["implicit"][0], "implicit_mask_gbs_cold": res["implicit"][1],
             "bytes_per_step": decode_bytes(window, mask_bytes=2 * (n0 + steps // 2))}
 
     if want("batched"):

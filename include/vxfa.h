@@ -104,6 +104,49 @@ int vxfa_flash_attn_ext(vxfa_ctx* ctx, const vxfa_tensor* q,
                         const vxfa_tensor* mask, vxfa_tensor* dst, float scale,
                         float max_bias, float logit_softcap, void* stream);
 
+/* Implicit masks. voxtral.cpp fills every mask it passes from a formula:
+ *   decoder prefill   causal [n, n]           fill_causal_mask,
+ *                                             src/voxtral.cpp:2104-2111
+ *                                             (used at :2421 and :2493)
+ *   realtime encoder  causal window of 750    src/voxtral.cpp:2179-2190
+ * then uploads it and casts it to F16 inside every layer's graph (:1564,
+ * :1801). A descriptor of the formula replaces the tensor: query row i
+ * (0-based along q's ne[1]) attends kv position j iff
+ *   j <= i + offset   and, when window > 0,   j >= i + offset - window + 1.
+ * (Decoder prefill: offset 0, window 0. Realtime encoder: offset 0, window
+ * 750. A decode step with a sliding window W over n_kv cached rows:
+ * offset n_kv - 1, window W.) The result equals vxfa_flash_attn_ext with an
+ * F16 mask [Nkv, Nq, 1, 1] holding 0 at those positions and -inf elsewhere.
+ * The kernels derive live ranges and tile classes from the formula instead
+ * of reading a mask, so no mask is filled, copied or scanned. */
+enum vxfa_mask_kind {
+    VXFA_MASK_NONE   = 0,  /* no mask: same as passing mask = NULL */
+    VXFA_MASK_CAUSAL = 1,  /* causal, optionally limited to a window */
+};
+
+typedef struct vxfa_mask_desc {
+    int32_t kind;    /* enum vxfa_mask_kind                                  */
+    int32_t window;  /* 0: unbounded; W > 0: the last W positions up to the
+                        diagonal                                             */
+    int64_t offset;  /* kv position on query row 0's diagonal                 */
+} vxfa_mask_desc;
+
+/* Validate a mask descriptor (pure host code). NULL is valid (no mask).
+ * Returns VXFA_OK or VXFA_INVALID_ARG. */
+int vxfa_check_mask_desc(const vxfa_mask_desc* mask);
+
+/* GGML_OP_FLASH_ATTN_EXT with an implicit mask (see above) in place of the
+ * mask tensor; otherwise the same contract, status codes and stream
+ * behaviour as vxfa_flash_attn_ext. No counterpart in ggml's op: it is for a
+ * caller that owns the mask's formula (voxtral.cpp's builders at
+ * src/voxtral.cpp:1801 and :1564 would pass a descriptor instead of the
+ * cast mask tensor). mask = NULL or kind VXFA_MASK_NONE means no mask. */
+int vxfa_flash_attn_ext_implicit(vxfa_ctx* ctx, const vxfa_tensor* q,
+                                 const vxfa_tensor* k, const vxfa_tensor* v,
+                                 const vxfa_mask_desc* mask, vxfa_tensor* dst,
+                                 float scale, float max_bias,
+                                 float logit_softcap, void* stream);
+
 /* Human-readable name of a status code (static storage). */
 const char* vxfa_status_str(int status);
 

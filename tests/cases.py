@@ -152,6 +152,27 @@ def prefill_case(n=439, hq=32, hkv=8, hd=128, seed=3, causal=True, kv_offset=0, 
     return c
 
 
+def implicit_mask(nq, nkv, offset, window=0):
+    """The explicit F16 mask [nq, nkv] that an implicit causal / window mask
+    descriptor stands for (include/vxfa.h): row i attends j iff
+    j <= i + offset and, for window > 0, j >= i + offset - window + 1."""
+    qi = np.arange(nq, dtype=np.int64)[:, None] + offset
+    ki = np.arange(nkv, dtype=np.int64)[None, :]
+    allow = ki <= qi
+    if window > 0:
+        allow &= ki >= qi - window + 1
+    return np.where(allow, np.uint16(0), NEG_INF_F16).astype(np.uint16)
+
+
+def with_mask(c: Case, m: np.ndarray) -> Case:
+    """Attach (or replace) an explicit mask [nq, nkv] broadcast over heads and batch."""
+    nq, nkv = m.shape
+    c.bufs.pop("mask", None)
+    c.views.pop("mask", None)
+    c.add("mask", "mask", np.ascontiguousarray(m), F16, *views.mask(nkv, nq))
+    return c
+
+
 def batched_case(n_streams=32, hq=32, hkv=8, hd=128, capacity=8192, lo=512, hi=8192, seed=5,
                  kv_sigma=0.5, name=None):
     """32 independent decode streams along ne[3] with ragged valid lengths

@@ -48,6 +48,25 @@ class Runner:
         assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
         return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy()
 
+    def run_implicit(self, case, mask_desc, dev=None, check=True):
+        """The case's q/k/v through vxfa_flash_attn_ext_implicit (its mask
+        tensor, if any, is not passed)."""
+        dev = dev if dev is not None else to_device(case)
+        d = descs(case, dev)
+        B, Nq, Hq, D = case.out_shape
+        n = B * Nq * Hq * D
+        buf = torch.from_numpy(np.full(n + 2 * CANARY, CANARY_BITS, dtype=np.uint32)).to("cuda")
+        ne, nb = case.dst_ne_nb()
+        dst = vxfa.desc(buf.data_ptr() + 4 * CANARY, vxfa.F32, ne, nb)
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = self.ctx.flash_attn_ext_implicit(d["q"], d["k"], d["v"], mask_desc, dst, case.scale,
+                                              stream=stream, check=check)
+        torch.cuda.synchronize()
+        host = buf.cpu().numpy()
+        assert (host[:CANARY] == CANARY_BITS).all(), "write before dst"
+        assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
+        return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy()
+
     def close(self):
         self.ctx.close()
 

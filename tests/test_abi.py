@@ -6,6 +6,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 import cases
@@ -125,3 +126,51 @@ def test_zero_sized_query_is_accepted():
     b, t, ne, nb, off = c.views["q"]
     c.views["q"] = (b, t, (ne[0], ne[1], ne[2], 0), nb, off)
     assert supports(c) == vxfa.OK
+
+
+# --- implicit masks (vxfa_flash_attn_ext_implicit) ----------------------------
+
+def test_mask_desc_layout_matches_header():
+    # int32 kind; int32 window; int64 offset
+    assert ctypes.sizeof(vxfa.VxfaMaskDesc) == 16
+    assert vxfa.VxfaMaskDesc.window.offset == 4 and vxfa.VxfaMaskDesc.offset.offset == 8
+
+
+def test_mask_desc_validation():
+    assert vxfa.check_mask_desc(None) == vxfa.OK
+    assert vxfa.check_mask_desc(vxfa.mask_desc(vxfa.MASK_NONE)) == vxfa.OK
+    assert vxfa.check_mask_desc(vxfa.mask_desc(vxfa.MASK_CAUSAL, 0, 0)) == vxfa.OK
+    assert vxfa.check_mask_desc(vxfa.mask_desc(vxfa.MASK_CAUSAL, 750, -5)) == vxfa.OK
+    assert vxfa.check_mask_desc(vxfa.mask_desc(2)) == vxfa.INVALID_ARG
+    assert vxfa.check_mask_desc(vxfa.mask_desc(vxfa.MASK_CAUSAL, -1, 0)) == vxfa.INVALID_ARG
+
+
+def test_implicit_entry_rejects_a_null_context():
+    # returns before any HIP call
+    lib = vxfa.load()
+    m = vxfa.mask_desc()
+    assert lib.vxfa_flash_attn_ext_implicit(None, None, None, None, ctypes.byref(m), None,
+                                            0.125, 0.0, 0.0, None) == vxfa.INVALID_ARG
+
+
+def test_implicit_mask_formula_matches_voxtral_masks():
+    """The descriptor's formula reproduces the masks voxtral.cpp fills:
+    fill_causal_mask (src/voxtral.cpp:2104-2111, built by prefill_case), the
+    realtime encoder window (:2179-2190, built by encoder_case), the decode
+    window of the streaming workload (built by decode_case) and a causal
+    prefill against a filled cache (kv_offset rows before the chunk)."""
+    def mask_of(c):
+        b, _, ne, _, _ = c.views["mask"]
+        return c.bufs[b].reshape(-1, ne[0])
+    n = 75
+    assert np.array_equal(cases.implicit_mask(n, n, 0), mask_of(cases.prefill_case(n, hq=4, hkv=1, hd=64)))
+    pc = cases.prefill_case(20, hq=4, hkv=1, hd=64, kv_offset=33)
+    assert np.array_equal(cases.implicit_mask(20, 53, 33), mask_of(pc))
+    ec = cases.encoder_case(90, 2, 64, window=17)
+    assert np.array_equal(cases.implicit_mask(90, 90, 0, 17), mask_of(ec))
+    dc = cases.decode_case(300, hq=4, hkv=1, hd=64, window=64)
+    assert np.array_equal(cases.implicit_mask(1, 300, 299, 64), mask_of(dc))
+    # closed forms: window 1 keeps only the diagonal; a negative offset empties the first rows
+    assert (cases.implicit_mask(8, 8, 0, 1) == 0).sum() == 8
+    m = cases.implicit_mask(8, 8, -3)
+    assert (m[:3] == cases.NEG_INF_F16).all() and (m[3] == 0).sum() == 1

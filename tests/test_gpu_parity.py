@@ -301,3 +301,92 @@ def test_graph_capture_replays_match_eager(runner):
         for o, ref, c in zip(outs, eager, cs):
             got = o.cpu().numpy().reshape(c.out_shape)
             assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (rep, c.name)
+
+
+# --- implicit masks: vxfa_flash_attn_ext_implicit ------------------------------
+# The descriptor path against the explicit mask tensor it stands for (same
+# case, same device bytes) and against the oracle run with that tensor.
+# Prefill takes the same kernel path with the same step order, so the bits
+# must agree exactly; decode sizes its splits to the live range instead of
+# n_kv, which changes the summation order, so it is held to the parity bar.
+
+def _implicit(runner, c, offset, window=0, bitwise=True):
+    import gpu_util
+    from conftest import load_package
+    vx = load_package().vxfa
+    B, Nq, Hq, D = c.out_shape
+    nkv = c.views["k"][2][1]
+    cases.with_mask(c, cases.implicit_mask(Nq, nkv, offset, window))
+    _say(f"[implicit] {c.name} offset={offset} window={window}")
+    explicit = check_case(runner, c)
+    dev = gpu_util.to_device(c)
+    rc, out = runner.run_implicit(c, vx.mask_desc(vx.MASK_CAUSAL, window, offset), dev=dev)
+    assert rc == 0
+    assert np.isfinite(out).all()
+    if bitwise:
+        assert np.array_equal(out.view(np.uint32), explicit.view(np.uint32))
+    m, r, ok = gpu_util.parity(out, cases.oracle_f64(c), ATOL, RTOL)
+    _say(f"    implicit vs f64 maxabs={m:.3e} rel={r:.3e}; vs explicit maxabs={np.abs(out - explicit).max():.3e}")
+    assert ok, (m, r)
+    return out
+
+
+def test_implicit_decoder_prefill_439_causal(runner):
+    _implicit(runner, cases.prefill_case(439, seed=41, causal=False), offset=0)
+
+
+@pytest.mark.parametrize("n,kv_offset", [(64, 448), (1, 100), (200, 37)])
+def test_implicit_causal_against_filled_cache(runner, n, kv_offset):
+    c = cases.prefill_case(n, seed=42 + n, causal=False, kv_offset=kv_offset)
+    _implicit(runner, c, offset=kv_offset, bitwise=(n > 1))
+
+
+def test_implicit_realtime_encoder_window(runner):
+    """Realtime encoder: 32 heads, hd 64, causal window 750 (src/voxtral.cpp:2179-2190)."""
+    _implicit(runner, cases.encoder_case(1100, 32, 64, seed=43), offset=0, window=750)
+
+
+@pytest.mark.parametrize("window", [1, 100, 512])
+def test_implicit_prefill_windows(runner, window):
+    _implicit(runner, cases.prefill_case(333, seed=44, causal=False), offset=0, window=window)
+
+
+def test_implicit_negative_offset_empties_rows(runner):
+    out = _implicit(runner, cases.prefill_case(130, seed=45, causal=False), offset=-5)
+    assert (out[:, :5] == 0).all()
+
+
+def test_implicit_decode_sliding_window(runner):
+    """Config 4 shape: cache 16384, n_kv 16285, window 2048 as a descriptor."""
+    c = cases.decode_case(16285, capacity=16384, seed=46)
+    _implicit(runner, c, offset=16284, window=2048, bitwise=False)
+
+
+@pytest.mark.parametrize("n_kv,offset,window", [(1024, 1023, 0), (777, 500, 64), (300, 5000, 0), (300, -1, 0)])
+def test_implicit_decode_ranges(runner, n_kv, offset, window):
+    c = cases.decode_case(n_kv, seed=47 + n_kv)
+    out = _implicit(runner, c, offset=offset, window=window, bitwise=False)
+    if offset < 0:
+        assert (out == 0).all()
+
+
+def test_implicit_none_equals_no_mask(runner):
+    import gpu_util
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.encoder_case(300, 4, 64, seed=48)
+    dev = gpu_util.to_device(c)
+    rc1, a = runner.run(c, dev=dev)
+    rc2, b = runner.run_implicit(c, vx.mask_desc(vx.MASK_NONE), dev=dev)
+    rc3, d = runner.run_implicit(c, None, dev=dev)
+    assert rc1 == rc2 == rc3 == 0
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), d.view(np.uint32))
+
+
+def test_implicit_rejects_bad_descriptor(runner):
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.decode_case(64, seed=49)
+    rc, _ = runner.run_implicit(c, vx.mask_desc(7, 0, 0), check=False)
+    assert rc == vx.INVALID_ARG

@@ -35,6 +35,14 @@ struct AttnArgs {
     int32_t n_split;      // decode: workgroups per (batch, kv head)
     int32_t mask_vec;     // mask data and strides 16-byte aligned (128-bit mask loads)
     float scale_log2;     // scale * log2(e)
+    // implicit causal / window mask (instead of a mask tensor): query row i
+    // attends kv j iff j <= i + im_offset and, when im_window > 0,
+    // j >= i + im_offset - im_window + 1
+    int32_t im_causal;
+    int32_t im_window;
+    int64_t im_offset;
+    // decode without a mask tensor: the live kv range [kv_lo, kv_hi)
+    int32_t kv_lo, kv_hi;
 };
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -87,72 +95,59 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
-// Eight consecutive F16 mask entries starting at p, as four 32-bit words
-// (entry e in half e % 2 of word e / 2). Entries at or past `valid` read as
-// -inf. The widest load the address allows is used: 16, 4 or 2 bytes.
-__device__ __forceinline__ u32x4 load_mask8(const uint16_t* p, int valid) {
-    const uint32_t dead = 0xFC00FC00u;
-    u32x4 w = {dead, dead, dead, dead};
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
-    if (valid >= 8 && (addr & 15) == 0) {
-        w = *reinterpret_cast<const u32x4*>(p);
-    } else if (valid >= 8 && (addr & 3) == 0) {
-        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-        w = u32x4{q[0], q[1], q[2], q[3]};
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t h = e < valid ? (uint32_t)p[e] : (uint32_t)kF16NegInf;
-            w[e >> 1] = (e & 1) ? ((w[e >> 1] & 0xFFFFu) | (h << 16)) : ((w[e >> 1] & 0xFFFF0000u) | h);
-        }
-    }
-    return w;
-}
-
-// Bit e set when entry e of the eight is not -inf.
-__device__ __forceinline__ uint32_t live_bits8(u32x4 w) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m |= ((w[i] & 0xFFFFu) != kF16NegInf ? 1u : 0u) << (2 * i);
-        m |= ((w[i] >> 16) != kF16NegInf ? 1u : 0u) << (2 * i + 1);
-    }
-    return m;
-}
-
 // Live range [lo, hi) over `rows` mask rows of n entries each (row r at
 // base + r * row_stride bytes): lo is the first and hi - 1 the last column
 // holding an entry other than -inf in any of the rows; lo = hi = 0 when every
 // entry is -inf. Every thread of the block calls it and gets the result.
-// Rows are cut into 8-entry chunks; each thread takes whole chunks, four at a
-// time with all loads issued before any test, so the scan costs a few memory
-// round trips whatever the row alignment. red: 2 ints of LDS per wavefront.
+// Each row is read as the 16-byte-aligned chunks that cover it, whatever the
+// row's alignment: a chunk holds at least one byte of the row, so it lies in
+// the same 16-byte granule (same allocation, same page) as mask data, and
+// entries outside the row are dropped in registers. A thread takes chunks
+// tid, tid + NT, ... eight at a time, all eight loads issued before any is
+// tested (a 16K-entry row at 256 threads is one memory round trip). A chunk
+// of eight -inf entries is recognised with two word compares; only chunks
+// holding a live entry work out its first and last column.
+// red: 2 ints of LDS per wavefront.
 template <int NT>
 __device__ __forceinline__ void mask_live_range(const uint16_t* base, int64_t row_stride, int rows, int n, int* red,
                                                 int& lo, int& hi) {
+    constexpr int U = 8;
     const int tid = threadIdx.x;
-    const int nch = (n + 7) >> 3;
-    const int items = rows * nch;
+    // chunks per row: exact when every row has the first row's alignment
+    const int mis0 = (int)(reinterpret_cast<uintptr_t>(base) & 15);
+    const int ncr = (rows == 1 || (row_stride & 15) == 0) ? (mis0 + 2 * n + 15) / 16 : (2 * n + 15) / 16 + 1;
+    const int items = rows * ncr;
+    constexpr uint32_t DEAD = 0xFC00FC00u;
     int tlo = 0x7fffffff, thi = -1;
-    for (int i0 = tid; i0 < items; i0 += 4 * NT) {
-        u32x4 w[4];
-        int col[4];
+    for (int i0 = tid; i0 < items; i0 += U * NT) {
+        u32x4 w[U];
+        int col[U];   // row column of the chunk's first entry (may be < 0); n when unused
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int i = i0 + u * NT;
-            col[u] = -1;
-            w[u] = u32x4{0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u};
-            if (i < items) {
-                const int r = i / nch, c = i - r * nch;
-                col[u] = 8 * c;
-                const uint16_t* p = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) +
-                                                                      (int64_t)r * row_stride) + 8 * c;
-                w[u] = load_mask8(p, n - 8 * c);
-            }
+            const int r = i / ncr, c = i - r * ncr;
+            const char* rowp = reinterpret_cast<const char*>(base) + (int64_t)r * row_stride;
+            const int off = 16 * c - (int)(reinterpret_cast<uintptr_t>(rowp) & 15);   // bytes from the row start
+            const bool ok = i < items && off < 2 * n;
+            col[u] = ok ? off / 2 : n;
+            w[u] = u32x4{DEAD, DEAD, DEAD, DEAD};
+            if (ok) w[u] = *reinterpret_cast<const u32x4*>(rowp + off);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t m = live_bits8(w[u]);
+        for (int u = 0; u < U; ++u) {
+            if ((w[u][0] & w[u][1]) == DEAD && (w[u][2] & w[u][3]) == DEAD &&
+                (w[u][0] | w[u][1] | w[u][2] | w[u][3]) == DEAD)
+                continue;   // eight -inf entries
+            uint32_t m = 0;   // bit e: entry e is not -inf
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                m |= ((w[u][j] & 0xFFFFu) != kF16NegInf ? 1u : 0u) << (2 * j);
+                m |= ((w[u][j] >> 16) != kF16NegInf ? 1u : 0u) << (2 * j + 1);
+            }
+            if (col[u] < 0 || col[u] > n - 8) {   // a chunk reaching outside the row
+                const int e_lo = min(max(-col[u], 0), 8), e_hi = min(max(n - col[u], 0), 8);
+                m &= e_hi > e_lo ? ((1u << (e_hi - e_lo)) - 1u) << e_lo : 0u;
+            }
             if (m) {
                 tlo = min(tlo, col[u] + (int)__builtin_ctz(m));
                 thi = max(thi, col[u] + 31 - (int)__builtin_clz(m));

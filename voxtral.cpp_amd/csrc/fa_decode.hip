@@ -39,7 +39,10 @@
 //         shared by the wavefront (DPP row reductions).
 // Masks: an additive F16 mask is honoured exactly (-inf removes a position).
 // The workgroup first scans the mask row(s) for the live range, so a sliding
-// window or a ragged stream length only costs its live positions.
+// window or a ragged stream length only costs its live positions. Without a
+// mask tensor the host passes the live range (all of n_kv, or the rows an
+// implicit causal / window mask leaves to the query) and sizes the splits to
+// it, so no scan runs.
 #include "fa_common.h"
 
 namespace vxfa {
@@ -76,7 +79,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     // ---- live range of the KV axis -------------------------------------
     // The mask rows of this group's query heads: planes (g G + j) % hm of
     // batch b % bm. One scan when they are one plane or consecutive planes.
-    int lo = 0, hi = a.nkv;
+    int lo = a.kv_lo, hi = a.kv_hi;   // without a mask tensor the host gives the live range
     if constexpr (masked) {
         const char* mb = (const char*)a.mask + (int64_t)(b % a.bm) * a.m_nb3;
         const int p0 = (g * G) % a.hm;

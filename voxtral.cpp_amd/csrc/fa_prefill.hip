@@ -161,9 +161,17 @@ __device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t ro
     if (thi < 0) { lo = 0; hi = 0; } else { lo = 64 * tlo; hi = min(64 * thi + 64, n); }
 }
 
-template <int D, int NQW, int KVG, bool MASK, bool QF16>
+// MM: 0 no mask, 1 an F16 mask tensor, 2 an implicit causal / window mask
+// (query row i attends kv j iff j <= i + offset and, with a window W,
+// j >= i + offset - W + 1), which equals the tensor holding 0 there and -inf
+// elsewhere; its live range and tile classes follow from the formula, and a
+// mixed tile's mask words are formed in registers, bit for bit those the
+// tensor would give.
+template <int D, int NQW, int KVG, int MM, bool QF16>
 __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, int nqt) {
     static_assert(D == 64 || D == 128, "head dim");
+    constexpr bool MASK = MM != 0;
+    constexpr bool IMPL = MM == 2;
     constexpr int NW = NQW * KVG;      // wavefronts
     constexpr int NT = 64 * NW;
     constexpr int BM = 32 * NQW;
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     __shared__ __attribute__((aligned(16))) char sK[2 * TILE_BYTES];
     __shared__ float s_ml[KVG > 1 ? 2 * (KVG - 1) * NQW * 64 : 1];
     __shared__ int s_red[2 * NW];
-    __shared__ uint8_t s_tflag[MASK ? NQW * PF_MAXT : 1];
+    __shared__ uint8_t s_tflag[MM == 1 ? NQW * PF_MAXT : 1];
 
     // ---- XCD-aware position of this workgroup --------------------------------
     const int nwg = gridDim.x;
@@ -236,7 +244,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // diagonal of a causal mask, the edges of a window) read mask values.
     const uint16_t* mplane = nullptr;
     int step_lo = 0, step_hi = nstep;
-    if (MASK) {
+    if constexpr (MM == 1) {
         mplane = (const uint16_t*)((const char*)a.mask + (int64_t)(h % a.hm) * a.m_nb2 +
                                    (int64_t)(b % a.bm) * a.m_nb3);
         int lo = 0, hi = 0;
@@ -245,6 +253,19 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
                                  a.nkv, s_tflag, s_red, lo, hi);
         step_lo = lo / BS;
         step_hi = hi > lo ? (hi - 1) / BS + 1 : 0;
+    } else if constexpr (IMPL) {
+        // rows q0 .. q_last attend [q0 + offset - W + 1, q_last + offset]
+        const int64_t q_last = (int64_t)min(q0 + BM, a.nq) - 1;
+        int64_t lo = a.im_window > 0 ? (int64_t)q0 + a.im_offset - a.im_window + 1 : 0;
+        int64_t hi = q_last + a.im_offset + 1;
+        lo = lo < 0 ? 0 : lo;
+        hi = hi > a.nkv ? a.nkv : hi;
+        if (hi > lo) {
+            step_lo = (int)(lo / BS);
+            step_hi = (int)((hi - 1) / BS) + 1;
+        } else {
+            step_lo = step_hi = 0;
+        }
     }
     // Step sequence. Without a mask: every step, the last one (which holds
     // the partial tile when n_kv % 64 != 0) last, the others rotated by the
@@ -342,7 +363,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // mask row of this lane's query (rows past n_q read row 0: their results
     // are never stored)
     const uint16_t* mrow = nullptr;
-    if (MASK) mrow = (const uint16_t*)((const char*)mplane + (int64_t)(qvalid ? qrow : 0) * a.m_nb1);
+    if (MM == 1) mrow = (const uint16_t*)((const char*)mplane + (int64_t)(qvalid ? qrow : 0) * a.m_nb1);
     const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     const float c = a.scale_log2;
 
@@ -352,7 +373,25 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // row-to-KV mapping, so its two 16-byte loads come swapped. Positions
     // past n_kv read as -inf.
     auto load_mask = [&](int kv0, uint32_t (&mw)[2][8]) {
-        if (a.mask_vec && kv0 + PF_BN <= a.nkv) {
+        if constexpr (IMPL) {
+            // implicit: 0 where the row attends kv, -inf elsewhere (and past
+            // n_kv); rows past n_q use row 0, as the tensor path reads
+            const int64_t last = (int64_t)(qvalid ? qrow : 0) + a.im_offset;
+            const int64_t first = a.im_window > 0 ? last - a.im_window + 1 : INT64_MIN;
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                for (int w = 0; w < 8; ++w) {
+                    uint32_t pair = 0;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int kv = kv0 + 32 * kvb + pf_kv_of(hh, 2 * w + e);
+                        const bool live = kv < a.nkv && (int64_t)kv <= last && (int64_t)kv >= first;
+                        pair |= (live ? 0u : (uint32_t)kF16NegInf) << (16 * e);
+                    }
+                    mw[kvb][w] = pair;
+                }
+        } else if (a.mask_vec && kv0 + PF_BN <= a.nkv) {
 #pragma unroll
             for (int kvb = 0; kvb < 2; ++kvb) {
                 const uint16_t* p = mrow + kv0 + 32 * kvb + 16 * hh;
@@ -497,8 +536,19 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // class of this wavefront's tile at kv0 (MASK only): 1 all zero, 2 or 0
     // dead, 3 mixed
     auto tclass = [&](int kv0) -> int {
-        const int t = kv0 / PF_BN;
-        return t < PF_MAXT ? (int)s_tflag[qw * PF_MAXT + t] : 3;
+        if constexpr (IMPL) {
+            const int64_t r0 = q0 + 32 * qw;                           // this wavefront's rows
+            const int64_t r1 = (int64_t)min(q0 + 32 * qw + 32, a.nq) - 1;
+            if (r1 < r0) return 0;
+            const int64_t c0 = kv0, c1 = (int64_t)min(kv0 + PF_BN, a.nkv) - 1;   // the tile's columns
+            const int64_t off = a.im_offset, W = a.im_window;
+            if (c0 > r1 + off || (W > 0 && c1 < r0 + off - W + 1)) return 2;
+            const bool all = c1 <= r0 + off && (W == 0 || c0 >= r1 + off - W + 1);
+            return (all && kv0 + PF_BN <= a.nkv) ? 1 : 3;
+        } else {
+            const int t = kv0 / PF_BN;
+            return t < PF_MAXT ? (int)s_tflag[qw * PF_MAXT + t] : 3;
+        }
     };
     auto run_tile = [&](int stg, int kv0, const uint32_t (&mw)[2][8]) {
         if constexpr (MASK) {
@@ -610,7 +660,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     }
 }
 
-template <int D, int NQW, int KVG, bool MASK>
+template <int D, int NQW, int KVG, int MM>
 static hipError_t launch_pw(const AttnArgs& a, hipStream_t st) {
     constexpr int BM = 32 * NQW;
     const int nqt = (a.nq + BM - 1) / BM;
@@ -618,24 +668,29 @@ static hipError_t launch_pw(const AttnArgs& a, hipStream_t st) {
     if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
     constexpr int NT = 64 * NQW * KVG;
     const dim3 grid((unsigned)nwg), block(NT);
-    if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MASK, true>), grid, block, 0, st, a, nqt);
-    else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MASK, false>), grid, block, 0, st, a, nqt);
+    if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, true>), grid, block, 0, st, a, nqt);
+    else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, false>), grid, block, 0, st, a, nqt);
     return hipGetLastError();
 }
 
 // waves = query-row wavefronts per workgroup (32 rows each); 0 picks the
 // default. hd 64 without a mask: 4 (16 wavefronts with their 3 KV partners,
 // 4 per SIMD) or 2. hd 64 with a mask keeps its mask words in registers and
-// always runs 2 (8 wavefronts). hd 128: 4 or 2 with one KV partner each.
+// always runs 2 (8 wavefronts). hd 128: 4 or 2 with one KV partner each; with
+// a mask (tensor or implicit) always 2.
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t st) {
-    const bool mask = a.mask != nullptr;
+    const int mm = a.im_causal ? 2 : (a.mask != nullptr ? 1 : 0);
     if (head_dim == 64) {
-        if (mask) return launch_pw<64, 2, 4, true>(a, st);
-        if (waves == 0 || waves == 4) return launch_pw<64, 4, 4, false>(a, st);
-        if (waves == 2) return launch_pw<64, 2, 4, false>(a, st);
+        if (mm == 1) return launch_pw<64, 2, 4, 1>(a, st);
+        if (mm == 2) return launch_pw<64, 2, 4, 2>(a, st);
+        if (waves == 0 || waves == 4) return launch_pw<64, 4, 4, 0>(a, st);
+        if (waves == 2) return launch_pw<64, 2, 4, 0>(a, st);
     } else if (head_dim == 128) {
-        if (waves == 0 || waves == 4) return mask ? launch_pw<128, 4, 2, true>(a, st) : launch_pw<128, 4, 2, false>(a, st);
-        if (waves == 2) return mask ? launch_pw<128, 2, 2, true>(a, st) : launch_pw<128, 2, 2, false>(a, st);
+        // masked hd 128 always runs 2 (with 4 its registers spill)
+        if (mm == 1) return launch_pw<128, 2, 2, 1>(a, st);
+        if (mm == 2) return launch_pw<128, 2, 2, 2>(a, st);
+        if (waves == 0 || waves == 4) return launch_pw<128, 4, 2, 0>(a, st);
+        if (waves == 2) return launch_pw<128, 2, 2, 0>(a, st);
     }
     return hipErrorInvalidValue;
 }

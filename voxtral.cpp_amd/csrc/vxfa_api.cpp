@@ -36,7 +36,8 @@ struct vxfa_ctx {
 
 namespace {
 
-constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
+constexpr int kVersion = 1 * 10000 + 1 * 100 + 0;
+constexpr int kMaskedSplitCap = 32;
 
 void set_err(vxfa_ctx* c, const char* fmt, ...) {
     if (!c) return;
@@ -127,12 +128,15 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
 }
 
 // Workgroups per (batch, kv head) for the decode split kernel: 2048
-// wavefronts in all (8 per CU), at least one 32-position tile per wavefront,
-// and at most kDecodeMaxSplit so the merge stays short.
+// wavefronts in all (8 per CU), at least 64 live positions per workgroup
+// (two of its wavefronts busy: more, smaller splits finish sooner when the
+// range is short), and at most kDecodeMaxSplit so the merge stays short.
+// With a mask tensor every split workgroup scans the whole mask row, so the
+// caller caps the count (measured on a 2048 window of a 16K cache).
 int choose_split(int64_t pairs, int64_t nkv) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
-    const int64_t by_len = (nkv + 32 * vxfa::kDecodeWaves - 1) / (32 * vxfa::kDecodeWaves);
+    const int64_t by_len = (nkv + 63) / 64;
     if (s > by_len) s = by_len;
     if (s > 64) s = 64;
     if (s < 1) s = 1;
@@ -190,9 +194,15 @@ const char* vxfa_last_error(const vxfa_ctx* c) { return c ? c->last_error : ""; 
 
 int vxfa_version(void) { return kVersion; }
 
-int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v,
-                        const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap,
-                        void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The op, with either a mask tensor (`mask`), an implicit causal / window mask
+// (`im`, kind VXFA_MASK_CAUSAL) or neither; never both (the entry points
+// enforce it).
+int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
+        const vxfa_mask_desc* im, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream) {
     if (!c) return VXFA_INVALID_ARG;
     c->last_error[0] = 0;
     const char* why = nullptr;
@@ -201,6 +211,7 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
         set_err(c, "%s", why);
         return rc;
     }
+    const bool implicit = im != nullptr && im->kind == VXFA_MASK_CAUSAL;
     const int64_t D = q->ne[0], Nq = q->ne[1], Hq = q->ne[2], B = q->ne[3];
     const int64_t Nkv = k->ne[1], Hkv = k->ne[2];
     if (Nq * Hq * B == 0) return VXFA_OK;
@@ -234,10 +245,29 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
     a.mask_vec = mask && aligned16(mask->data, 0) && !(mask->nb[1] & 15) && !(mask->nb[2] & 15) &&
                  !(mask->nb[3] & 15);
     a.scale_log2 = scale * vxfa::kLog2e;
+    a.kv_lo = 0;
+    a.kv_hi = (int32_t)Nkv;
+    if (implicit) {
+        a.im_causal = 1;
+        a.im_window = im->window;
+        a.im_offset = im->offset;
+    }
 
     const int64_t G = Hq / Hkv;
     if (Nq == 1 && (G == 1 || G == 2 || G == 4)) {
-        int S = choose_split(B * Hkv, Nkv);
+        if (implicit) {
+            // the one query row attends [offset - W + 1, offset], clipped to [0, n_kv)
+            int64_t lo = im->window > 0 ? im->offset - im->window + 1 : 0;
+            int64_t hi = im->offset + 1;
+            lo = lo < 0 ? 0 : lo;
+            hi = hi > Nkv ? Nkv : hi;
+            if (hi <= lo) lo = hi = 0;
+            a.kv_lo = (int32_t)lo;
+            a.kv_hi = (int32_t)hi;
+            a.im_causal = 0;   // the range is all the decode kernel needs
+        }
+        int S = choose_split(B * Hkv, a.kv_hi - a.kv_lo);
+        if (mask && S > kMaskedSplitCap) S = kMaskedSplitCap;
         if (c->split_override > 0) S = c->split_override < vxfa::kDecodeMaxSplit ? c->split_override : vxfa::kDecodeMaxSplit;
         a.n_split = S;
         if (S > 1) {
@@ -260,7 +290,7 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
             a.ws = c->ws;
         }
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
-    } else if (D == 64 && !mask && scale != 0.0f && c->pp_enabled) {
+    } else if (D == 64 && !mask && !implicit && scale != 0.0f && c->pp_enabled) {
         // (scale 0 goes to the general kernel: the pipelined one folds the
         // scale into the exponent and scores the partial block's dead rows -inf)
         // encoder prefill: the software-pipelined hd 64 kernel
@@ -279,6 +309,34 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
         return VXFA_HIP_ERROR;
     }
     return VXFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v,
+                        const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap,
+                        void* stream) {
+    return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream);
+}
+
+int vxfa_check_mask_desc(const vxfa_mask_desc* m) {
+    if (!m) return VXFA_OK;
+    if (m->kind != VXFA_MASK_NONE && m->kind != VXFA_MASK_CAUSAL) return VXFA_INVALID_ARG;
+    if (m->window < 0) return VXFA_INVALID_ARG;
+    return VXFA_OK;
+}
+
+int vxfa_flash_attn_ext_implicit(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v,
+                                 const vxfa_mask_desc* mask, vxfa_tensor* dst, float scale, float max_bias,
+                                 float logit_softcap, void* stream) {
+    if (!c) return VXFA_INVALID_ARG;
+    if (vxfa_check_mask_desc(mask) != VXFA_OK) {
+        set_err(c, "mask descriptor: kind must be VXFA_MASK_NONE or VXFA_MASK_CAUSAL and window >= 0");
+        return VXFA_INVALID_ARG;
+    }
+    return run(c, q, k, v, nullptr, mask, dst, scale, max_bias, logit_softcap, stream);
 }
 
 }  // extern "C"

@@ -17,12 +17,16 @@ F32, F16 = 0, 1  # equal to ggml's GGML_TYPE_F32 / GGML_TYPE_F16
 
 OK, UNSUPPORTED, INVALID_ARG, NO_WORKSPACE, HIP_ERROR = 0, 1, 2, 3, 4
 
+MASK_NONE, MASK_CAUSAL = 0, 1  # enum vxfa_mask_kind
+
 # every symbol include/vxfa.h declares
 EXPORTS = (
     "vxfa_ctx_create",
     "vxfa_ctx_destroy",
     "vxfa_supports",
     "vxfa_flash_attn_ext",
+    "vxfa_check_mask_desc",
+    "vxfa_flash_attn_ext_implicit",
     "vxfa_status_str",
     "vxfa_last_error",
     "vxfa_version",
@@ -37,6 +41,22 @@ class VxfaTensor(ctypes.Structure):
         ("ne", ctypes.c_int64 * 4),
         ("nb", ctypes.c_size_t * 4),
     ]
+
+
+class VxfaMaskDesc(ctypes.Structure):
+    """vxfa_mask_desc: query row i attends kv j iff j <= i + offset and, for
+    window > 0, j >= i + offset - window + 1."""
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("offset", ctypes.c_int64),
+    ]
+
+
+def mask_desc(kind: int = MASK_CAUSAL, window: int = 0, offset: int = 0) -> VxfaMaskDesc:
+    m = VxfaMaskDesc()
+    m.kind, m.window, m.offset = int(kind), int(window), int(offset)
+    return m
 
 
 class VxfaError(RuntimeError):
@@ -67,6 +87,12 @@ def load() -> ctypes.CDLL:
     L.vxfa_flash_attn_ext.argtypes = [ctypes.c_void_p, P, P, P, P, P, ctypes.c_float, ctypes.c_float,
                                       ctypes.c_float, ctypes.c_void_p]
     L.vxfa_flash_attn_ext.restype = ctypes.c_int
+    M = ctypes.POINTER(VxfaMaskDesc)
+    L.vxfa_check_mask_desc.argtypes = [M]
+    L.vxfa_check_mask_desc.restype = ctypes.c_int
+    L.vxfa_flash_attn_ext_implicit.argtypes = [ctypes.c_void_p, P, P, P, M, P, ctypes.c_float, ctypes.c_float,
+                                               ctypes.c_float, ctypes.c_void_p]
+    L.vxfa_flash_attn_ext_implicit.restype = ctypes.c_int
     L.vxfa_status_str.argtypes = [ctypes.c_int]
     L.vxfa_status_str.restype = ctypes.c_char_p
     L.vxfa_last_error.argtypes = [ctypes.c_void_p]
@@ -99,6 +125,11 @@ def _ref(t):
     return ctypes.byref(t) if t is not None else None
 
 
+def check_mask_desc(m) -> int:
+    """Host-only validation of a mask descriptor (VxfaMaskDesc or None)."""
+    return load().vxfa_check_mask_desc(_ref(m))
+
+
 def supports(q, k, v, mask, dst, scale: float, max_bias: float = 0.0, logit_softcap: float = 0.0) -> int:
     """Host-only capability check (ggml supports_op analogue)."""
     return load().vxfa_supports(_ref(q), _ref(k), _ref(v), _ref(mask), _ref(dst), scale, max_bias, logit_softcap)
@@ -117,6 +148,15 @@ class Context:
                        logit_softcap: float = 0.0, stream: int = 0, check: bool = True) -> int:
         rc = self._lib.vxfa_flash_attn_ext(self._h, _ref(q), _ref(k), _ref(v), _ref(mask), _ref(dst),
                                            scale, max_bias, logit_softcap, ctypes.c_void_p(stream))
+        if check and rc != OK:
+            raise VxfaError(rc, self.last_error())
+        return rc
+
+    def flash_attn_ext_implicit(self, q, k, v, mask_desc, dst, scale: float, max_bias: float = 0.0,
+                                logit_softcap: float = 0.0, stream: int = 0, check: bool = True) -> int:
+        """The op with an implicit causal / window mask (a VxfaMaskDesc, or None)."""
+        rc = self._lib.vxfa_flash_attn_ext_implicit(self._h, _ref(q), _ref(k), _ref(v), _ref(mask_desc), _ref(dst),
+                                                    scale, max_bias, logit_softcap, ctypes.c_void_p(stream))
         if check and rc != OK:
             raise VxfaError(rc, self.last_error())
         return rc
