@@ -67,11 +67,12 @@ def randn(torch, shape, seed, sigma=1.0, dtype=None):
 class Layer:
     """Descriptors of one flash_attn_ext call plus the tensors behind them."""
 
-    def __init__(self, q, k, v, mask, dst, scale, keep, md=None):
+    def __init__(self, q, k, v, mask, dst, scale, keep, md=None, kn=None, vn=None, fused=True):
         self.q, self.k, self.v, self.mask, self.dst = q, k, v, mask, dst
         self.scale = scale
         self.keep = keep
         self.md = md   # vxfa_mask_desc for the implicit-mask entry point, else None
+        self.kn, self.vn, self.fused = kn, vn, fused   # new K/V rows (F32) to append first, else None
 
 
 def f32s(x):
@@ -157,6 +158,11 @@ def time_calls(torch, ctx, calls, steps, warmup, graph=True):
 
     def one_step(sh):
         for L in calls:
+            if L.kn is not None and L.fused:   # append fused into the attention call
+                ctx.flash_attn_ext_append(L.q, L.k, L.v, L.kn, L.vn, L.mask, L.dst, L.scale, stream=sh)
+                continue
+            if L.kn is not None:   # append, then attention: two calls
+                ctx.kv_append(L.kn, L.vn, L.k, L.v, stream=sh)
             if L.md is not None:   # implicit causal / window mask
                 ctx.flash_attn_ext_implicit(L.q, L.k, L.v, L.md, L.dst, L.scale, stream=sh)
             else:
@@ -322,6 +328,22 @@ def main():
             log(f"[decode n_kv={n_kv}] {us:.2f} us/layer  {gbs:.0f} GB/s")
             configs[f"decode_nkv{n_kv}"] = {"us_per_layer": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
                                             "bytes_per_layer": by, "layers": layers, "cache": "cold (30 layers)"}
+            if n_kv == 8192:
+                # the new token's K/V (F32, one 1024-float row each) appended to the f16 cache:
+                # fused into the attention launch, and as a separate append launch
+                news = [(randn(torch, (1024,), 7000 + 2 * i), randn(torch, (1024,), 7001 + 2 * i))
+                        for i in range(layers)]
+                row = lambda t: vxfa.desc(t.data_ptr(), vxfa.F32, (1024, 1, 1, 1), (4, 4096, 4096, 4096))
+                res_app = {}
+                for fused in (True, False):
+                    calls = [Layer(L.q, L.k, L.v, None, L.dst, L.scale, L.keep, None, row(kn), row(vn), fused)
+                             for L, (kn, vn) in zip(dl, news)]
+                    _, res_app[fused] = time_calls(torch, ctx, calls, K, W)
+                log(f"[decode n_kv=8192 + append] fused {res_app[True]:.2f} us/layer; "
+                    f"append launch + attention {res_app[False]:.2f} us/layer")
+                configs["decode_nkv8192"].update({"append_fused_us_per_layer": res_app[True],
+                                                  "append_separate_us_per_layer": res_app[False]})
+                del news
             del dl
             torch.cuda.empty_cache()
 

@@ -147,6 +147,34 @@ int vxfa_flash_attn_ext_implicit(vxfa_ctx* ctx, const vxfa_tensor* q,
                                  float scale, float max_bias,
                                  float logit_softcap, void* stream);
 
+/* F16 KV cache append. build_decoder_layer stores each layer's new keys and
+ * values with two ggml_cpy nodes into cache views (src/voxtral.cpp:1758-1770);
+ * with an F16 cache these are F32 -> F16 conversions (round to nearest even,
+ * overflow to inf). k_new, v_new: F32 [Hkv * D, n_new, 1, Bk], rows
+ * contiguous (kv head h at elements h * D .. h * D + D - 1, the layout of
+ * the reshape at :1743); k, v: the F16 cache views [D, n_kv, Hkv, Bk] the
+ * attention op reads (:1773-1794). Rows n_kv - n_new .. n_kv - 1 of k and v
+ * receive the new rows (voxtral's n_kv = kv_offset + n_tokens).
+ * One launch for K and V; asynchronous on `stream`. */
+int vxfa_kv_append(vxfa_ctx* ctx, const vxfa_tensor* k_new,
+                   const vxfa_tensor* v_new, vxfa_tensor* k, vxfa_tensor* v,
+                   void* stream);
+
+/* vxfa_kv_append(k_new, v_new, k, v) followed by vxfa_flash_attn_ext(q, k,
+ * v, mask, dst, ...), with the same result bits. For a single-token decode
+ * step (Nq = 1, n_new = 1) the append is fused into the attention kernel:
+ * the new row is read once from the F32 source, used, and written to the
+ * cache by the same launch; otherwise the append kernel runs first on the
+ * same stream. No counterpart in ggml's op: it replaces the two ggml_cpy
+ * nodes plus the attention node of each decoder layer (:1758-1802). */
+int vxfa_flash_attn_ext_append(vxfa_ctx* ctx, const vxfa_tensor* q,
+                               vxfa_tensor* k, vxfa_tensor* v,
+                               const vxfa_tensor* k_new,
+                               const vxfa_tensor* v_new,
+                               const vxfa_tensor* mask, vxfa_tensor* dst,
+                               float scale, float max_bias,
+                               float logit_softcap, void* stream);
+
 /* Human-readable name of a status code (static storage). */
 const char* vxfa_status_str(int status);
 

@@ -67,6 +67,41 @@ class Runner:
         assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
         return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy()
 
+    def run_append(self, case, k_new, v_new, fused=True, check=True):
+        """Append the F32 rows k_new / v_new ([Bk, n_new, Hkv * D]) to the last
+        rows of the case's k/v cache views and attend: one
+        vxfa_flash_attn_ext_append call (fused=True) or vxfa_kv_append then
+        vxfa_flash_attn_ext. Returns (rc, out, device buffers after the call)."""
+        dev = to_device(case)
+        d = descs(case, dev)
+        kn = torch.from_numpy(np.ascontiguousarray(k_new, dtype=np.float32)).to("cuda")
+        vn = torch.from_numpy(np.ascontiguousarray(v_new, dtype=np.float32)).to("cuda")
+        bk, n_new, row = k_new.shape
+        ne = (row, n_new, 1, bk)
+        nb = (4, 4 * row, 4 * row * n_new, 4 * row * n_new)
+        dkn = vxfa.desc(kn.data_ptr(), vxfa.F32, ne, nb)
+        dvn = vxfa.desc(vn.data_ptr(), vxfa.F32, ne, nb)
+        B, Nq, Hq, D = case.out_shape
+        n = B * Nq * Hq * D
+        buf = torch.from_numpy(np.full(n + 2 * CANARY, CANARY_BITS, dtype=np.uint32)).to("cuda")
+        dne, dnb = case.dst_ne_nb()
+        dst = vxfa.desc(buf.data_ptr() + 4 * CANARY, vxfa.F32, dne, dnb)
+        stream = torch.cuda.current_stream().cuda_stream
+        if fused:
+            rc = self.ctx.flash_attn_ext_append(d["q"], d["k"], d["v"], dkn, dvn, d.get("mask"), dst, case.scale,
+                                                stream=stream, check=check)
+        else:
+            rc = self.ctx.kv_append(dkn, dvn, d["k"], d["v"], stream=stream, check=check)
+            if rc == 0:
+                rc = self.ctx.flash_attn_ext(d["q"], d["k"], d["v"], d.get("mask"), dst, case.scale,
+                                             stream=stream, check=check)
+        torch.cuda.synchronize()
+        host = buf.cpu().numpy()
+        assert (host[:CANARY] == CANARY_BITS).all(), "write before dst"
+        assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
+        after = {name: t.cpu().numpy() for name, t in dev.items()}
+        return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy(), after
+
     def close(self):
         self.ctx.close()
 

@@ -174,3 +174,10 @@ def test_implicit_mask_formula_matches_voxtral_masks():
     assert (cases.implicit_mask(8, 8, 0, 1) == 0).sum() == 8
     m = cases.implicit_mask(8, 8, -3)
     assert (m[:3] == cases.NEG_INF_F16).all() and (m[3] == 0).sum() == 1
+
+
+def test_append_entries_reject_a_null_context():
+    lib = vxfa.load()
+    assert lib.vxfa_kv_append(None, None, None, None, None, None) == vxfa.INVALID_ARG
+    assert lib.vxfa_flash_attn_ext_append(None, None, None, None, None, None, None, None,
+                                          0.1, 0.0, 0.0, None) == vxfa.INVALID_ARG

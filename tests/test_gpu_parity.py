@@ -390,3 +390,116 @@ def test_implicit_rejects_bad_descriptor(runner):
     c = cases.decode_case(64, seed=49)
     rc, _ = runner.run_implicit(c, vx.mask_desc(7, 0, 0), check=False)
     assert rc == vx.INVALID_ARG
+
+
+# --- f16 KV cache append: vxfa_kv_append / vxfa_flash_attn_ext_append ---------
+# New K/V rows arrive as F32 (the projections of build_decoder_layer) and are
+# rounded to f16 into the cache (the ggml_cpy of src/voxtral.cpp:1758-1770).
+# The cache bytes after the call must equal numpy's float16 (round to nearest
+# even) of the rows, every other cache byte untouched; the attention output is
+# checked against the oracle run on that appended cache.
+
+def _append_rows(rng, bk, n_new, row, special=False):
+    k = rng.standard_normal((bk, n_new, row)).astype(np.float32)
+    v = rng.standard_normal((bk, n_new, row)).astype(np.float32)
+    if special:   # overflow to inf, subnormals, an exact tie, negative zero
+        k[0, 0, :6] = [70000.0, -1e6, 3e-6, -6e-8, np.float32(1.0 + 2.0 ** -11), -0.0]
+    return k, v
+
+
+def _expected_cache(c, k_new, v_new):
+    """The case with its cache rows n_kv - n_new .. n_kv - 1 set to f16(new)."""
+    import copy
+    e = copy.deepcopy(c)
+    bk, n_new, row = k_new.shape
+    for role, new in (("k", k_new), ("v", v_new)):
+        b, t, ne, nb, off = e.views[role]
+        D, nkv, hkv, _ = ne
+        raw = e.bufs[b].view(np.uint8).reshape(-1).copy()
+        with np.errstate(over="ignore"):
+            bits = new.astype(np.float16).view(np.uint16)        # RNE, overflow -> inf
+        for bb in range(bk):
+            for tt in range(n_new):
+                pos = nkv - n_new + tt
+                for h in range(hkv):
+                    at = off + pos * nb[1] + h * nb[2] + bb * nb[3]
+                    raw[at:at + 2 * D] = bits[bb, tt, h * D:(h + 1) * D].view(np.uint8)
+        e.bufs[b] = raw.view(e.bufs[b].dtype).reshape(e.bufs[b].shape)
+    return e
+
+
+def _check_append(runner, c, k_new, v_new, fused=True):
+    import gpu_util
+    e = _expected_cache(c, k_new, v_new)
+    _say(f"[append] {c.name} n_new={k_new.shape[1]} bk={k_new.shape[0]} fused={fused}")
+    rc, out, after = runner.run_append(c, k_new, v_new, fused=fused)
+    assert rc == 0
+    for role in ("k", "v"):
+        b = c.views[role][0]
+        assert np.array_equal(after[b], e.bufs[b].view(np.uint8).reshape(-1)), f"{role} cache bytes"
+    exact = cases.oracle_f64(e)
+    m, r, ok = gpu_util.parity(out, exact, ATOL, RTOL)
+    _say(f"    vs f64 on the appended cache maxabs={m:.3e} rel={r:.3e}")
+    assert np.isfinite(out).all() and ok, (m, r)
+    return out
+
+
+def test_kv_append_rows_bit_exact(runner):
+    import torch
+    import gpu_util
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.decode_case(40, hq=16, hkv=8, hd=128, capacity=64, seed=61)
+    k_new, v_new = _append_rows(np.random.default_rng(61), 1, 3, 8 * 128, special=True)
+    e = _expected_cache(c, k_new, v_new)
+    dev = gpu_util.to_device(c)
+    d = gpu_util.descs(c, dev)
+    kn = torch.from_numpy(k_new).to("cuda")
+    vn = torch.from_numpy(v_new).to("cuda")
+    ne, nb = (1024, 3, 1, 1), (4, 4096, 12288, 12288)
+    rc = runner.ctx.kv_append(vx.desc(kn.data_ptr(), vx.F32, ne, nb), vx.desc(vn.data_ptr(), vx.F32, ne, nb),
+                              d["k"], d["v"], stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    for role in ("k", "v"):
+        b = c.views[role][0]
+        assert np.array_equal(dev[b].cpu().numpy(), e.bufs[b].view(np.uint8).reshape(-1)), role
+
+
+@pytest.mark.parametrize("n_kv", [1, 33, 1024, 8192])
+def test_fused_decode_append(runner, n_kv):
+    c = cases.decode_case(n_kv, capacity=n_kv + 16, seed=62 + n_kv)
+    k_new, v_new = _append_rows(np.random.default_rng(n_kv), 1, 1, 8 * 128)
+    fused = _check_append(runner, c, k_new, v_new, fused=True)
+    separate = _check_append(runner, c, k_new, v_new, fused=False)
+    assert np.abs(fused - separate).max() <= 1e-5
+
+
+def test_fused_decode_append_groups_and_batch(runner):
+    c = cases.decode_case(700, hq=16, hkv=8, hd=64, capacity=720, batch=3, seed=63)
+    k_new, v_new = _append_rows(np.random.default_rng(63), 3, 1, 8 * 64)
+    _check_append(runner, c, k_new, v_new, fused=True)
+
+
+def test_fused_decode_append_masked(runner):
+    """Streaming shape with an explicit window mask over the appended row."""
+    c = cases.decode_case(5000, capacity=5008, window=1024, seed=64)
+    k_new, v_new = _append_rows(np.random.default_rng(64), 1, 1, 8 * 128)
+    _check_append(runner, c, k_new, v_new, fused=True)
+
+
+def test_prefill_append_matches_separate(runner):
+    c = cases.prefill_case(64, seed=65, kv_offset=448)
+    k_new, v_new = _append_rows(np.random.default_rng(65), 1, 64, 8 * 128)
+    a = _check_append(runner, c, k_new, v_new, fused=True)
+    b = _check_append(runner, c, k_new, v_new, fused=False)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_append_rejects_bad_rows(runner):
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.decode_case(64, seed=66)
+    k_new, v_new = _append_rows(np.random.default_rng(66), 1, 1, 8 * 128 + 8)   # wrong row length
+    rc, _, _ = runner.run_append(c, k_new, v_new, fused=True, check=False)
+    assert rc == vx.INVALID_ARG

@@ -43,6 +43,26 @@ struct AttnArgs {
     int64_t im_offset;
     // decode without a mask tensor: the live kv range [kv_lo, kv_hi)
     int32_t kv_lo, kv_hi;
+    // decode with a fused KV append: the row at n_kv - 1 of k and v is the new
+    // token's, taken from the F32 sources k_new / v_new (kv head h at floats
+    // h * D .. h * D + D - 1 of the token row; per kv batch nb3 bytes apart),
+    // rounded to f16 and also written into k and v
+    int32_t append;
+    const float* k_new;
+    const float* v_new;
+    int64_t kn_nb3, vn_nb3;
+};
+
+// F32 -> F16 append of new K/V rows into the cache (the ggml_cpy of
+// src/voxtral.cpp:1758-1770 into an f16 cache).
+struct AppendArgs {
+    const float* k_new;   // [Hkv * D] per token row, rows kn_nb1 apart, batches kn_nb3 apart
+    const float* v_new;
+    int64_t kn_nb1, kn_nb3, vn_nb1, vn_nb3;
+    _Float16* k;          // cache views [D, n_kv, Hkv, Bk] (byte strides)
+    _Float16* v;
+    int64_t k_nb1, k_nb2, k_nb3, v_nb1, v_nb2, v_nb3;
+    int32_t d, hkv, n_new, pos0, bk;   // rows pos0 .. pos0 + n_new - 1 are written
 };
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -245,4 +265,5 @@ constexpr int dec_record_floats(int D, int G) { return G * D + ((2 * G + 3) & ~3
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
 hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
+hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
 }  // namespace vxfa

@@ -100,7 +100,12 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         }
     }
 
-    const int span = hi - lo;
+    // With a fused append the new row (n_kv - 1) is not read from the cache:
+    // every workgroup walks [lo, hi_main) and wavefront 0 of the last split
+    // folds the new row in afterwards, from the F32 source.
+    const bool new_live = a.append && hi == a.nkv;
+    const int hi_main = a.append ? min(hi, a.nkv - 1) : hi;
+    const int span = max(hi_main - lo, 0);
     const int ntiles = (span + DEC_TILE - 1) / DEC_TILE;
     const int t_begin = (int)(((int64_t)ntiles * split) / a.n_split);
     const int t_end = (int)(((int64_t)ntiles * (split + 1)) / a.n_split);
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     };
     auto load_tile = [&](Tile& T, int t) {
         const int p0 = lo + t * DEC_TILE;
-        const int pend = min(p0 + DEC_TILE, hi);
+        const int pend = min(p0 + DEC_TILE, hi_main);
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
             const int pos = min(p0 + 16 * grp + (lane & 15), pend - 1);
@@ -201,9 +206,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
 
-    auto process = [&](const Tile& T, int tt) {
-        const int p0 = lo + tt * DEC_TILE;
-        const int pend = min(p0 + DEC_TILE, hi);
+    auto process = [&](const Tile& T, int p0, int pend) {
         floatx4 sc[2];
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
@@ -263,13 +266,56 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     while (t < t_end) {
         int tn = t + DEC_WAVES;
         if (tn < t_end) load_tile(TB, tn);
-        process(TA, t);
+        process(TA, lo + t * DEC_TILE, min(lo + t * DEC_TILE + DEC_TILE, hi_main));
         t = tn;
         if (t >= t_end) break;
         tn = t + DEC_WAVES;
         if (tn < t_end) load_tile(TA, tn);
-        process(TB, t);
+        process(TB, lo + t * DEC_TILE, min(lo + t * DEC_TILE + DEC_TILE, hi_main));
         t = tn;
+    }
+
+    // ---- fused append: the new row, from the F32 sources --------------------
+    // Every lane reads the new row in its own K and V operand layout (all
+    // positions of the one-row tile clamp to it; only position n_kv - 1 is
+    // valid in process()), rounded to f16 exactly as the cache will hold it.
+    // The lanes holding each element once write the rounded row to the cache.
+    if (a.append && split == a.n_split - 1 && wave == 0) {
+        const int pn = a.nkv - 1;
+        const float* kn = (const float*)((const char*)a.k_new + (int64_t)bkv * a.kn_nb3) + g * D;
+        const float* vn = (const float*)((const char*)a.v_new + (int64_t)bkv * a.vn_nb3) + g * D;
+        auto cvt8 = [](const float* p) {
+            const floatx4 x0 = *(const floatx4*)p, x1 = *(const floatx4*)(p + 4);
+            half8 y;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                y[i] = (_Float16)x0[i];
+                y[4 + i] = (_Float16)x1[i];
+            }
+            return y;
+        };
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 kx = cvt8(kn + kcol + 32 * ks);
+            TA.k[0][ks] = kx;
+            TA.k[1][ks] = kx;
+        }
+        const half8 vx = cvt8(vn + vcol);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) TA.v[i] = vx;
+        if constexpr (masked) {
+#pragma unroll
+            for (int grp = 0; grp < 2; ++grp)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) TA.m[grp][i] = mplane[i][pn];
+        }
+        if (new_live) process(TA, pn, pn + 1);
+        if ((lane & 15) == 0) {
+            _Float16* kc = (_Float16*)(kb + (int64_t)pn * a.k_nb1) + kcol;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) *(half8*)(kc + 32 * ks) = TA.k[0][ks];
+        }
+        if (lane < CH) *(half8*)((_Float16*)(vb + (int64_t)pn * a.v_nb1) + vcol) = vx;
     }
 
     // ---- merge lanes, then wavefronts ------------------------------------

@@ -133,6 +133,62 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
 // range is short), and at most kDecodeMaxSplit so the merge stays short.
 // With a mask tensor every split workgroup scans the whole mask row, so the
 // caller caps the count (measured on a 2048 window of a 16K cache).
+// New K/V rows for an append: F32 [Hkv * D, n_new, 1, Bk] with contiguous
+// 16-byte-aligned rows, going to the last n_new rows of the F16 cache views
+// k, v [D, n_kv, Hkv, Bk] (checked by check()).
+int check_append(const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* kn, const vxfa_tensor* vn,
+                 const char** why) {
+    if (!kn || !vn) { *why = "k_new and v_new are required"; return VXFA_INVALID_ARG; }
+    const vxfa_tensor* nw[2] = {kn, vn};
+    const vxfa_tensor* cache[2] = {k, v};
+    for (int i = 0; i < 2; ++i) {
+        const vxfa_tensor* t = nw[i];
+        for (int d = 0; d < 4; ++d)
+            if (t->ne[d] < 0) { *why = "negative ne"; return VXFA_INVALID_ARG; }
+        if (t->ne[0] != cache[i]->ne[0] * cache[i]->ne[2]) { *why = "new rows must hold Hkv * D elements"; return VXFA_INVALID_ARG; }
+        if (t->ne[1] > cache[i]->ne[1]) { *why = "more new rows than cache rows"; return VXFA_INVALID_ARG; }
+        if (t->ne[2] != 1 || t->ne[3] != cache[i]->ne[3]) { *why = "new rows must be [Hkv*D, n, 1, Bk]"; return VXFA_INVALID_ARG; }
+        if (t->type != VXFA_TYPE_F32) { *why = "new rows must be F32"; return VXFA_UNSUPPORTED; }
+        if (t->nb[0] != 4 || !aligned16(t->data, 0) || (t->nb[1] & 15) || (t->nb[3] & 15)) {
+            *why = "new rows must be contiguous and 16-byte aligned";
+            return VXFA_UNSUPPORTED;
+        }
+        if (cache[i]->type != VXFA_TYPE_F16) { *why = "the cache must be F16"; return VXFA_UNSUPPORTED; }
+        if (cache[i]->ne[0] % 8 || cache[i]->nb[0] != 2 || !aligned16(cache[i]->data, 0) || (cache[i]->nb[1] & 15) ||
+            (cache[i]->nb[2] & 15) || (cache[i]->nb[3] & 15)) {
+            *why = "cache rows must be contiguous and 16-byte aligned";
+            return VXFA_UNSUPPORTED;
+        }
+    }
+    if (kn->ne[1] != vn->ne[1]) { *why = "k_new and v_new row counts differ"; return VXFA_INVALID_ARG; }
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3] || k->ne[0] != v->ne[0]) {
+        *why = "k and v cache views differ";
+        return VXFA_INVALID_ARG;
+    }
+    if (kn->ne[1] > 0x7fffffff || k->ne[3] > 65535) { *why = "sizes beyond the launch limits"; return VXFA_UNSUPPORTED; }
+    return VXFA_OK;
+}
+
+vxfa::AppendArgs append_args(const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* kn,
+                             const vxfa_tensor* vn) {
+    vxfa::AppendArgs a;
+    memset(&a, 0, sizeof(a));
+    a.k_new = static_cast<const float*>(kn->data);
+    a.v_new = static_cast<const float*>(vn->data);
+    a.kn_nb1 = (int64_t)kn->nb[1]; a.kn_nb3 = (int64_t)kn->nb[3];
+    a.vn_nb1 = (int64_t)vn->nb[1]; a.vn_nb3 = (int64_t)vn->nb[3];
+    a.k = static_cast<_Float16*>(k->data);
+    a.v = static_cast<_Float16*>(v->data);
+    a.k_nb1 = (int64_t)k->nb[1]; a.k_nb2 = (int64_t)k->nb[2]; a.k_nb3 = (int64_t)k->nb[3];
+    a.v_nb1 = (int64_t)v->nb[1]; a.v_nb2 = (int64_t)v->nb[2]; a.v_nb3 = (int64_t)v->nb[3];
+    a.d = (int32_t)k->ne[0];
+    a.hkv = (int32_t)k->ne[2];
+    a.n_new = (int32_t)kn->ne[1];
+    a.pos0 = (int32_t)(k->ne[1] - kn->ne[1]);
+    a.bk = (int32_t)k->ne[3];
+    return a;
+}
+
 int choose_split(int64_t pairs, int64_t nkv) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
@@ -202,23 +258,34 @@ namespace {
 // (`im`, kind VXFA_MASK_CAUSAL) or neither; never both (the entry points
 // enforce it).
 int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
-        const vxfa_mask_desc* im, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream) {
+        const vxfa_mask_desc* im, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream,
+        const vxfa_tensor* k_new = nullptr, const vxfa_tensor* v_new = nullptr) {
     if (!c) return VXFA_INVALID_ARG;
     c->last_error[0] = 0;
     const char* why = nullptr;
-    const int rc = check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
+    int rc = check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
+    if (rc == VXFA_OK && k_new) rc = check_append(k, v, k_new, v_new, &why);
     if (rc != VXFA_OK) {
         set_err(c, "%s", why);
         return rc;
     }
+    const bool append = k_new != nullptr && k_new->ne[1] > 0;
     const bool implicit = im != nullptr && im->kind == VXFA_MASK_CAUSAL;
     const int64_t D = q->ne[0], Nq = q->ne[1], Hq = q->ne[2], B = q->ne[3];
     const int64_t Nkv = k->ne[1], Hkv = k->ne[2];
-    if (Nq * Hq * B == 0) return VXFA_OK;
+    const int64_t Gq = Hq / Hkv;
+    // a single new row of a decode step is fused into the split kernel
+    const bool fuse_append = append && Nq == 1 && k_new->ne[1] == 1 && (Gq == 1 || Gq == 2 || Gq == 4) &&
+                             Nq * Hq * B > 0;
 
     hipError_t e = hipSetDevice(c->device);
     if (e != hipSuccess) { set_err(c, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (append && !fuse_append) {
+        e = vxfa::launch_kv_append(append_args(k, v, k_new, v_new), st);
+        if (e != hipSuccess) { set_err(c, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    }
+    if (Nq * Hq * B == 0) return VXFA_OK;
 
     if (Nkv == 0) {
         e = vxfa::launch_zero(static_cast<float*>(dst->data), Nq * Hq * B * D, st);
@@ -247,6 +314,13 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     a.scale_log2 = scale * vxfa::kLog2e;
     a.kv_lo = 0;
     a.kv_hi = (int32_t)Nkv;
+    if (fuse_append) {
+        a.append = 1;
+        a.k_new = static_cast<const float*>(k_new->data);
+        a.v_new = static_cast<const float*>(v_new->data);
+        a.kn_nb3 = (int64_t)k_new->nb[3];
+        a.vn_nb3 = (int64_t)v_new->nb[3];
+    }
     if (implicit) {
         a.im_causal = 1;
         a.im_window = im->window;
@@ -319,6 +393,36 @@ int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k,
                         const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap,
                         void* stream) {
     return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream);
+}
+
+int vxfa_kv_append(vxfa_ctx* c, const vxfa_tensor* k_new, const vxfa_tensor* v_new, vxfa_tensor* k, vxfa_tensor* v,
+                   void* stream) {
+    if (!c) return VXFA_INVALID_ARG;
+    c->last_error[0] = 0;
+    if (!k || !v) { set_err(c, "k and v are required"); return VXFA_INVALID_ARG; }
+    const char* why = nullptr;
+    const int rc = check_append(k, v, k_new, v_new, &why);
+    if (rc != VXFA_OK) {
+        set_err(c, "%s", why);
+        return rc;
+    }
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) { set_err(c, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    e = vxfa::launch_kv_append(append_args(k, v, k_new, v_new), reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) { set_err(c, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    return VXFA_OK;
+}
+
+int vxfa_flash_attn_ext_append(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, vxfa_tensor* v,
+                               const vxfa_tensor* k_new, const vxfa_tensor* v_new, const vxfa_tensor* mask,
+                               vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream) {
+    if (!c) return VXFA_INVALID_ARG;
+    if (!k_new || !v_new) {
+        c->last_error[0] = 0;
+        set_err(c, "k_new and v_new are required");
+        return VXFA_INVALID_ARG;
+    }
+    return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new);
 }
 
 int vxfa_check_mask_desc(const vxfa_mask_desc* m) {

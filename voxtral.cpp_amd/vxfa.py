@@ -27,6 +27,8 @@ EXPORTS = (
     "vxfa_flash_attn_ext",
     "vxfa_check_mask_desc",
     "vxfa_flash_attn_ext_implicit",
+    "vxfa_kv_append",
+    "vxfa_flash_attn_ext_append",
     "vxfa_status_str",
     "vxfa_last_error",
     "vxfa_version",
@@ -93,6 +95,11 @@ def load() -> ctypes.CDLL:
     L.vxfa_flash_attn_ext_implicit.argtypes = [ctypes.c_void_p, P, P, P, M, P, ctypes.c_float, ctypes.c_float,
                                                ctypes.c_float, ctypes.c_void_p]
     L.vxfa_flash_attn_ext_implicit.restype = ctypes.c_int
+    L.vxfa_kv_append.argtypes = [ctypes.c_void_p, P, P, P, P, ctypes.c_void_p]
+    L.vxfa_kv_append.restype = ctypes.c_int
+    L.vxfa_flash_attn_ext_append.argtypes = [ctypes.c_void_p, P, P, P, P, P, P, P, ctypes.c_float, ctypes.c_float,
+                                             ctypes.c_float, ctypes.c_void_p]
+    L.vxfa_flash_attn_ext_append.restype = ctypes.c_int
     L.vxfa_status_str.argtypes = [ctypes.c_int]
     L.vxfa_status_str.restype = ctypes.c_char_p
     L.vxfa_last_error.argtypes = [ctypes.c_void_p]
@@ -157,6 +164,23 @@ class Context:
         """The op with an implicit causal / window mask (a VxfaMaskDesc, or None)."""
         rc = self._lib.vxfa_flash_attn_ext_implicit(self._h, _ref(q), _ref(k), _ref(v), _ref(mask_desc), _ref(dst),
                                                     scale, max_bias, logit_softcap, ctypes.c_void_p(stream))
+        if check and rc != OK:
+            raise VxfaError(rc, self.last_error())
+        return rc
+
+    def kv_append(self, k_new, v_new, k, v, stream: int = 0, check: bool = True) -> int:
+        """F32 -> F16 append of new K/V rows into the last rows of the cache views k, v."""
+        rc = self._lib.vxfa_kv_append(self._h, _ref(k_new), _ref(v_new), _ref(k), _ref(v), ctypes.c_void_p(stream))
+        if check and rc != OK:
+            raise VxfaError(rc, self.last_error())
+        return rc
+
+    def flash_attn_ext_append(self, q, k, v, k_new, v_new, mask, dst, scale: float, max_bias: float = 0.0,
+                              logit_softcap: float = 0.0, stream: int = 0, check: bool = True) -> int:
+        """kv_append then flash_attn_ext, fused for a single-token decode step."""
+        rc = self._lib.vxfa_flash_attn_ext_append(self._h, _ref(q), _ref(k), _ref(v), _ref(k_new), _ref(v_new),
+                                                  _ref(mask), _ref(dst), scale, max_bias, logit_softcap,
+                                                  ctypes.c_void_p(stream))
         if check and rc != OK:
             raise VxfaError(rc, self.last_error())
         return rc
