@@ -67,12 +67,13 @@ def randn(torch, shape, seed, sigma=1.0, dtype=None):
 class Layer:
     """Descriptors of one flash_attn_ext call plus the tensors behind them."""
 
-    def __init__(self, q, k, v, mask, dst, scale, keep, md=None, kn=None, vn=None, fused=True):
+    def __init__(self, q, k, v, mask, dst, scale, keep, md=None, kn=None, vn=None, fused=True, ring=None):
         self.q, self.k, self.v, self.mask, self.dst = q, k, v, mask, dst
         self.scale = scale
         self.keep = keep
         self.md = md   # vxfa_mask_desc for the implicit-mask entry point, else None
         self.kn, self.vn, self.fused = kn, vn, fused   # new K/V rows (F32) to append first, else None
+        self.ring = ring   # vxfa_ring: k/v are a ring-buffer cache
 
 
 def f32s(x):
@@ -158,6 +159,9 @@ def time_calls(torch, ctx, calls, steps, warmup, graph=True):
 
     def one_step(sh):
         for L in calls:
+            if L.ring is not None:   # decode step over a ring-buffer cache (+ its new row)
+                ctx.flash_attn_ext_ring(L.q, L.k, L.v, L.ring, L.kn, L.vn, L.dst, L.scale, stream=sh)
+                continue
             if L.kn is not None and L.fused:   # append fused into the attention call
                 ctx.flash_attn_ext_append(L.q, L.k, L.v, L.kn, L.vn, L.mask, L.dst, L.scale, stream=sh)
                 continue
@@ -370,7 +374,9 @@ def main():
     if want("sliding"):
         cap, n0, window, steps = 16384, 16284, 2048, 100
         res = {}
-        for mode, ncache, implicit in (("cold", 8, False), ("warm", 1, False), ("implicit", 8, True)):
+        # cold: 40 caches, so the 100 steps' windows (40 x 8.4 MB) exceed the 256 MB MALL;
+        # warm: one cache, whose window stays MALL-resident from step to step
+        for mode, ncache, implicit in (("cold", 40, False), ("warm", 1, False), ("implicit", 40, True)):
             caches = decode_layers(torch, ncache, cap, capacity=cap, seed=4000)
             masks = []
             calls = []
@@ -390,6 +396,23 @@ def main():
             res[mode] = (us, by / (us * 1e-6) / 1e9)
             del caches, calls, masks
             torch.cuda.empty_cache()
+        # the same window kept as a 2048-row ring (logical row p at cache row
+        # (start + p) % 2048): each step drops the oldest row and appends its
+        # new one in the same launch; 40 rings (336 MB) keep the reads cold
+        nr = 40
+        rings = decode_layers(torch, nr, window, capacity=window, seed=4100)
+        news = [(randn(torch, (1024,), 8000 + 2 * t), randn(torch, (1024,), 8001 + 2 * t)) for t in range(steps)]
+        row = lambda t: vxfa.desc(t.data_ptr(), vxfa.F32, (1024, 1, 1, 1), (4, 4096, 4096, 4096))
+        calls = []
+        for t in range(steps):
+            L = rings[t % nr]
+            calls.append(Layer(L.q, L.k, L.v, None, L.dst, L.scale, None, None, row(news[t][0]), row(news[t][1]),
+                               True, vxfa.ring(t % window, window)))
+        _, us_ring = time_calls(torch, ctx, calls, max(1, K // 4), 1)
+        res["ring"] = (us_ring, decode_bytes(window) / (us_ring * 1e-6) / 1e9)
+        del rings, news, calls
+        torch.cuda.empty_cache()
+        log(f"[sliding window as a ring + append] {us_ring:.2f} us/step {res['ring'][1]:.0f} GB/s")
         log(f"[sliding window] cold {res['cold'][0]:.2f} us/step {res['cold'][1]:.0f} GB/s; "
             f"warm {res['warm'][0]:.2f} us/step; implicit mask (cold) {res['implicit'][0]:.2f} us/step")
         configs["sliding_window_decode_16k_w2048"] = {
@@ -397,6 +420,7 @@ def main():
             "frac_hbm_peak_cold": res["cold"][1] / HBM_PEAK_GBS,
             "us_per_step_warm": res["warm"][0], "gbs_warm": res["warm"][1], "steps": steps,
             "implicit_mask_us_per_step_cold": res["implicit"][0], "implicit_mask_gbs_cold": res["implicit"][1],
+            "ring_append_us_per_step_cold": res["ring"][0], "ring_append_gbs_cold": res["ring"][1],
             "bytes_per_step": decode_bytes(window, mask_bytes=2 * (n0 + steps // 2))}
 
     if want("batched"):

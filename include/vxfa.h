@@ -175,6 +175,37 @@ int vxfa_flash_attn_ext_append(vxfa_ctx* ctx, const vxfa_tensor* q,
                                float scale, float max_bias,
                                float logit_softcap, void* stream);
 
+/* KV cache as a ring buffer. Once its cache holds VOXTRAL_DEC_WINDOW rows,
+ * voxtral.cpp moves every layer's K and V one row to the left before each
+ * decode step (kv_cache_shift_left, src/voxtral.cpp:1237-1266, called at
+ * :2446-2449): (window - 1) rows per layer, K and V, on every token. With a
+ * ring the same step is O(1): logical position p (0 = oldest kept token)
+ * lives in cache row (start + p) mod capacity, so dropping the oldest row is
+ * start = (start + 1) mod capacity, and no row is moved or cleared (rows at
+ * logical positions >= n_kv are never read, which also makes the full-cache
+ * memset of clear_kv_cache, :1222-1235, unnecessary). */
+typedef struct vxfa_ring {
+    int64_t start;  /* cache row of logical position 0; 0 <= start < capacity */
+    int64_t n_kv;   /* rows in use (logical 0 .. n_kv - 1); <= capacity        */
+} vxfa_ring;
+
+/* A decode step over a ring: q [D, 1, Hq, B]; k, v the whole cache
+ * [D, capacity, Hkv, Bk] (F16); attention over logical positions
+ * 0 .. n_kv - 1 with no mask (voxtral's decode steps pass none, :1961,
+ * :2052). With k_new / v_new (F32 [Hkv * D, 1, 1, Bk], or both NULL) the
+ * step's new row is logical position n_kv - 1: it is rounded to f16, used
+ * and written to its ring row in the same launch (as
+ * vxfa_flash_attn_ext_append). The result equals vxfa_flash_attn_ext on a
+ * linear cache holding the same rows in logical order. Single-token decode
+ * with GQA group 1, 2 or 4 only (else VXFA_UNSUPPORTED). No counterpart in
+ * ggml's op: it replaces the host-side shift plus the attention node. */
+int vxfa_flash_attn_ext_ring(vxfa_ctx* ctx, const vxfa_tensor* q,
+                             vxfa_tensor* k, vxfa_tensor* v,
+                             const vxfa_ring* ring, const vxfa_tensor* k_new,
+                             const vxfa_tensor* v_new, vxfa_tensor* dst,
+                             float scale, float max_bias, float logit_softcap,
+                             void* stream);
+
 /* Human-readable name of a status code (static storage). */
 const char* vxfa_status_str(int status);
 

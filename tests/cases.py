@@ -173,6 +173,29 @@ def with_mask(c: Case, m: np.ndarray) -> Case:
     return c
 
 
+def ring_case(c: Case, capacity: int, start: int, seed=0) -> Case:
+    """The decode case c (a linear cache whose k/v views hold n_kv rows) laid
+    out as a ring of `capacity` rows: logical row p at cache row
+    (start + p) % capacity, every other row random f16. k/v views cover the
+    whole ring [D, capacity, Hkv, Bk]."""
+    import copy
+    rng = np.random.default_rng(seed)
+    r = copy.deepcopy(c)
+    r.name = f"{c.name}_ring{capacity}_at{start}"
+    for role in ("k", "v"):
+        b, t, ne, nb, off = c.views[role]
+        D, nkv, hkv, bk = ne
+        assert off == 0 and nkv <= capacity
+        lin = c.bufs[b].reshape(bk, -1, hkv, D)
+        ring = f16_bits(normal(rng, (bk, capacity, hkv, D)))
+        rows = (start + np.arange(nkv)) % capacity
+        ring[:, rows] = lin[:, :nkv]
+        r.bufs[b] = ring
+        rne, rnb = views.kv_cache(capacity, hkv, D, capacity, batch=bk)
+        r.views[role] = (b, t, rne, rnb, 0)
+    return r
+
+
 def batched_case(n_streams=32, hq=32, hkv=8, hd=128, capacity=8192, lo=512, hi=8192, seed=5,
                  kv_sigma=0.5, name=None):
     """32 independent decode streams along ne[3] with ragged valid lengths

@@ -102,6 +102,37 @@ class Runner:
         after = {name: t.cpu().numpy() for name, t in dev.items()}
         return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy(), after
 
+    def run_ring(self, case, ring_desc, k_new=None, v_new=None, check=True):
+        """vxfa_flash_attn_ext_ring over the case's k/v views (the whole ring),
+        optionally appending the F32 rows k_new / v_new ([Bk, 1, Hkv * D]).
+        Returns (rc, out, device buffers after the call)."""
+        dev = to_device(case)
+        d = descs(case, dev)
+        dkn = dvn = None
+        keep = []
+        if k_new is not None:
+            kn = torch.from_numpy(np.ascontiguousarray(k_new, dtype=np.float32)).to("cuda")
+            vn = torch.from_numpy(np.ascontiguousarray(v_new, dtype=np.float32)).to("cuda")
+            keep += [kn, vn]
+            bk, n_new, row = k_new.shape
+            ne, nb = (row, n_new, 1, bk), (4, 4 * row, 4 * row * n_new, 4 * row * n_new)
+            dkn = vxfa.desc(kn.data_ptr(), vxfa.F32, ne, nb)
+            dvn = vxfa.desc(vn.data_ptr(), vxfa.F32, ne, nb)
+        B, Nq, Hq, D = case.out_shape
+        n = B * Nq * Hq * D
+        buf = torch.from_numpy(np.full(n + 2 * CANARY, CANARY_BITS, dtype=np.uint32)).to("cuda")
+        dne, dnb = case.dst_ne_nb()
+        dst = vxfa.desc(buf.data_ptr() + 4 * CANARY, vxfa.F32, dne, dnb)
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = self.ctx.flash_attn_ext_ring(d["q"], d["k"], d["v"], ring_desc, dkn, dvn, dst, case.scale,
+                                          stream=stream, check=check)
+        torch.cuda.synchronize()
+        host = buf.cpu().numpy()
+        assert (host[:CANARY] == CANARY_BITS).all(), "write before dst"
+        assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
+        after = {name: t.cpu().numpy() for name, t in dev.items()}
+        return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy(), after
+
     def close(self):
         self.ctx.close()
 

@@ -181,3 +181,11 @@ def test_append_entries_reject_a_null_context():
     assert lib.vxfa_kv_append(None, None, None, None, None, None) == vxfa.INVALID_ARG
     assert lib.vxfa_flash_attn_ext_append(None, None, None, None, None, None, None, None,
                                           0.1, 0.0, 0.0, None) == vxfa.INVALID_ARG
+
+
+def test_ring_struct_and_null_context():
+    assert ctypes.sizeof(vxfa.VxfaRing) == 16 and vxfa.VxfaRing.n_kv.offset == 8
+    lib = vxfa.load()
+    r = vxfa.ring(0, 1)
+    assert lib.vxfa_flash_attn_ext_ring(None, None, None, None, ctypes.byref(r), None, None, None,
+                                        0.1, 0.0, 0.0, None) == vxfa.INVALID_ARG

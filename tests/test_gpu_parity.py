@@ -503,3 +503,78 @@ def test_append_rejects_bad_rows(runner):
     k_new, v_new = _append_rows(np.random.default_rng(66), 1, 1, 8 * 128 + 8)   # wrong row length
     rc, _, _ = runner.run_append(c, k_new, v_new, fused=True, check=False)
     assert rc == vx.INVALID_ARG
+
+
+# --- ring-buffer KV cache: vxfa_flash_attn_ext_ring -----------------------------
+# Logical row p lives in cache row (start + p) % capacity. The kernel walks the
+# logical rows in the same tiles as for a linear cache, so the output must be
+# bit-identical to vxfa_flash_attn_ext on the linear cache with the same rows.
+
+@pytest.mark.parametrize("n_kv,capacity,start", [(1000, 1024, 0), (1000, 1024, 500), (2048, 2048, 2047),
+                                                 (8192, 8192, 77), (1, 64, 63), (33, 40, 20)])
+def test_ring_equals_linear(runner, n_kv, capacity, start):
+    from conftest import load_package
+    vx = load_package().vxfa
+    lin = cases.decode_case(n_kv, seed=71 + n_kv)
+    _say(f"[ring] n_kv={n_kv} capacity={capacity} start={start}")
+    rc, ref = runner.run(lin)
+    assert rc == 0
+    rg = cases.ring_case(lin, capacity, start, seed=72)
+    rc, out, _ = runner.run_ring(rg, vx.ring(start, n_kv))
+    assert rc == 0
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_kv,capacity,start", [(512, 512, 300), (100, 128, 100), (4096, 8192, 6000)])
+def test_ring_fused_append(runner, n_kv, capacity, start):
+    """The step's new row lands in cache row (start + n_kv - 1) % capacity,
+    nothing else is written, and the output equals the linear fused append."""
+    from conftest import load_package
+    vx = load_package().vxfa
+    lin = cases.decode_case(n_kv, hq=32, hkv=8, hd=128, seed=73 + n_kv)
+    k_new, v_new = _append_rows(np.random.default_rng(74), 1, 1, 8 * 128)
+    rc, ref, _ = runner.run_append(lin, k_new, v_new, fused=True)
+    assert rc == 0
+    rg = cases.ring_case(lin, capacity, start, seed=75)
+    rc, out, after = runner.run_ring(rg, vx.ring(start, n_kv), k_new, v_new)
+    assert rc == 0
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    row = (start + n_kv - 1) % capacity
+    for role, new in (("k", k_new), ("v", v_new)):
+        b = rg.views[role][0]
+        expect = rg.bufs[b].copy()
+        expect[0, row] = new[0, 0].astype(np.float16).view(np.uint16).reshape(8, 128)
+        assert np.array_equal(after[b], expect.view(np.uint8).reshape(-1)), role
+
+
+def test_ring_as_sliding_window(runner):
+    """A 2048-row ring holding the window equals the explicit window mask over a 16K cache."""
+    import gpu_util
+    from conftest import load_package
+    vx = load_package().vxfa
+    big = cases.decode_case(16285, capacity=16384, window=2048, seed=76)
+    rc, ref = runner.run(big)
+    assert rc == 0
+    win = cases.decode_case(2048, seed=76)
+    win.bufs["q"] = big.bufs["q"]
+    for role in ("k", "v"):
+        b = big.views[role][0]
+        win.bufs[b] = big.bufs[b][:, 16285 - 2048:16285].copy()
+    rg = cases.ring_case(win, 2048, 1234, seed=77)
+    rc, out, _ = runner.run_ring(rg, vx.ring(1234, 2048))
+    assert rc == 0
+    m, r, ok = gpu_util.parity(out, ref, 1e-5, 1e-5)
+    _say(f"    ring vs 16K windowed decode maxabs={m:.3e} rel={r:.3e}")
+    assert ok
+
+
+def test_ring_rejects_bad_descriptors(runner):
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.ring_case(cases.decode_case(100, seed=78), 128, 0)
+    assert runner.run_ring(c, vx.ring(128, 100), check=False)[0] == vx.INVALID_ARG
+    assert runner.run_ring(c, vx.ring(0, 129), check=False)[0] == vx.INVALID_ARG
+    p = cases.ring_case(cases.decode_case(100, seed=79), 128, 5)
+    p.views["q"] = cases.prefill_case(4, seed=79, causal=False).views["q"]
+    p.bufs["q"] = cases.prefill_case(4, seed=79, causal=False).bufs["q"]
+    assert runner.run_ring(p, vx.ring(5, 100), check=False)[0] == vx.UNSUPPORTED

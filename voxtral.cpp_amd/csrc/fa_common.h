@@ -48,6 +48,9 @@ struct AttnArgs {
     // h * D .. h * D + D - 1 of the token row; per kv batch nb3 bytes apart),
     // rounded to f16 and also written into k and v
     int32_t append;
+    // decode over a ring buffer: logical position p is cache row
+    // (ring_start + p) mod ring_cap; 0, 0 = a plain cache
+    int32_t ring_start, ring_cap;
     const float* k_new;
     const float* v_new;
     int64_t kn_nb3, vn_nb3;

@@ -131,13 +131,20 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         half8 v[NV];
         uint16_t m[2][4];
     };
+    // cache row of logical position pos: pos itself, or in a ring of
+    // ring_cap rows starting at ring_start, (ring_start + pos) mod ring_cap
+    // (ring_cap = ring_start = 0 leaves pos unchanged)
+    auto row_of = [&](int pos) {
+        const int r = pos + a.ring_start;
+        return r >= a.ring_cap ? r - a.ring_cap : r;
+    };
     auto load_tile = [&](Tile& T, int t) {
         const int p0 = lo + t * DEC_TILE;
         const int pend = min(p0 + DEC_TILE, hi_main);
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
             const int pos = min(p0 + 16 * grp + (lane & 15), pend - 1);
-            const char* kp = kb + (int64_t)pos * a.k_nb1 + kcol * 2;
+            const char* kp = kb + (int64_t)row_of(pos) * a.k_nb1 + kcol * 2;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
             if constexpr (masked) {
@@ -148,7 +155,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int pos = min(p0 + vrow + i * RPI, pend - 1);
-            T.v[i] = *(const half8*)(vb + (int64_t)pos * a.v_nb1 + vcol * 2);
+            T.v[i] = *(const half8*)(vb + (int64_t)row_of(pos) * a.v_nb1 + vcol * 2);
         }
     };
 
@@ -311,11 +318,11 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         }
         if (new_live) process(TA, pn, pn + 1);
         if ((lane & 15) == 0) {
-            _Float16* kc = (_Float16*)(kb + (int64_t)pn * a.k_nb1) + kcol;
+            _Float16* kc = (_Float16*)(kb + (int64_t)row_of(pn) * a.k_nb1) + kcol;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) *(half8*)(kc + 32 * ks) = TA.k[0][ks];
         }
-        if (lane < CH) *(half8*)((_Float16*)(vb + (int64_t)pn * a.v_nb1) + vcol) = vx;
+        if (lane < CH) *(half8*)((_Float16*)(vb + (int64_t)row_of(pn) * a.v_nb1) + vcol) = vx;
     }
 
     // ---- merge lanes, then wavefronts ------------------------------------

@@ -259,12 +259,25 @@ namespace {
 // enforce it).
 int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
         const vxfa_mask_desc* im, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream,
-        const vxfa_tensor* k_new = nullptr, const vxfa_tensor* v_new = nullptr) {
+        const vxfa_tensor* k_new = nullptr, const vxfa_tensor* v_new = nullptr, const vxfa_ring* ring = nullptr) {
     if (!c) return VXFA_INVALID_ARG;
     c->last_error[0] = 0;
     const char* why = nullptr;
     int rc = check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
     if (rc == VXFA_OK && k_new) rc = check_append(k, v, k_new, v_new, &why);
+    if (rc == VXFA_OK && ring) {
+        const int64_t G = q->ne[2] / k->ne[2];
+        if (ring->start < 0 || ring->start >= k->ne[1] || ring->n_kv < 0 || ring->n_kv > k->ne[1]) {
+            why = "ring: need 0 <= start < capacity and 0 <= n_kv <= capacity";
+            rc = VXFA_INVALID_ARG;
+        } else if (k_new && k_new->ne[1] > ring->n_kv) {
+            why = "ring: more new rows than rows in use";
+            rc = VXFA_INVALID_ARG;
+        } else if (q->ne[1] != 1 || !(G == 1 || G == 2 || G == 4) || mask || (k_new && k_new->ne[1] != 1)) {
+            why = "ring: single-token decode (GQA group 1, 2 or 4) without a mask, at most one new row";
+            rc = VXFA_UNSUPPORTED;
+        }
+    }
     if (rc != VXFA_OK) {
         set_err(c, "%s", why);
         return rc;
@@ -272,7 +285,7 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     const bool append = k_new != nullptr && k_new->ne[1] > 0;
     const bool implicit = im != nullptr && im->kind == VXFA_MASK_CAUSAL;
     const int64_t D = q->ne[0], Nq = q->ne[1], Hq = q->ne[2], B = q->ne[3];
-    const int64_t Nkv = k->ne[1], Hkv = k->ne[2];
+    const int64_t Nkv = ring ? ring->n_kv : k->ne[1], Hkv = k->ne[2];
     const int64_t Gq = Hq / Hkv;
     // a single new row of a decode step is fused into the split kernel
     const bool fuse_append = append && Nq == 1 && k_new->ne[1] == 1 && (Gq == 1 || Gq == 2 || Gq == 4) &&
@@ -314,6 +327,10 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     a.scale_log2 = scale * vxfa::kLog2e;
     a.kv_lo = 0;
     a.kv_hi = (int32_t)Nkv;
+    if (ring) {
+        a.ring_start = (int32_t)ring->start;
+        a.ring_cap = (int32_t)k->ne[1];
+    }
     if (fuse_append) {
         a.append = 1;
         a.k_new = static_cast<const float*>(k_new->data);
@@ -423,6 +440,18 @@ int vxfa_flash_attn_ext_append(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k
         return VXFA_INVALID_ARG;
     }
     return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new);
+}
+
+int vxfa_flash_attn_ext_ring(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, vxfa_tensor* v, const vxfa_ring* ring,
+                             const vxfa_tensor* k_new, const vxfa_tensor* v_new, vxfa_tensor* dst, float scale,
+                             float max_bias, float logit_softcap, void* stream) {
+    if (!c) return VXFA_INVALID_ARG;
+    if (!ring || (k_new == nullptr) != (v_new == nullptr)) {
+        c->last_error[0] = 0;
+        set_err(c, "a ring descriptor is required; k_new and v_new come together");
+        return VXFA_INVALID_ARG;
+    }
+    return run(c, q, k, v, nullptr, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, ring);
 }
 
 int vxfa_check_mask_desc(const vxfa_mask_desc* m) {

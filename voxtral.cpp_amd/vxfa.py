@@ -29,6 +29,7 @@ EXPORTS = (
     "vxfa_flash_attn_ext_implicit",
     "vxfa_kv_append",
     "vxfa_flash_attn_ext_append",
+    "vxfa_flash_attn_ext_ring",
     "vxfa_status_str",
     "vxfa_last_error",
     "vxfa_version",
@@ -59,6 +60,20 @@ def mask_desc(kind: int = MASK_CAUSAL, window: int = 0, offset: int = 0) -> Vxfa
     m = VxfaMaskDesc()
     m.kind, m.window, m.offset = int(kind), int(window), int(offset)
     return m
+
+
+class VxfaRing(ctypes.Structure):
+    """vxfa_ring: logical position p lives in cache row (start + p) mod capacity."""
+    _fields_ = [
+        ("start", ctypes.c_int64),
+        ("n_kv", ctypes.c_int64),
+    ]
+
+
+def ring(start: int, n_kv: int) -> VxfaRing:
+    r = VxfaRing()
+    r.start, r.n_kv = int(start), int(n_kv)
+    return r
 
 
 class VxfaError(RuntimeError):
@@ -100,6 +115,9 @@ def load() -> ctypes.CDLL:
     L.vxfa_flash_attn_ext_append.argtypes = [ctypes.c_void_p, P, P, P, P, P, P, P, ctypes.c_float, ctypes.c_float,
                                              ctypes.c_float, ctypes.c_void_p]
     L.vxfa_flash_attn_ext_append.restype = ctypes.c_int
+    L.vxfa_flash_attn_ext_ring.argtypes = [ctypes.c_void_p, P, P, P, ctypes.POINTER(VxfaRing), P, P, P,
+                                           ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
+    L.vxfa_flash_attn_ext_ring.restype = ctypes.c_int
     L.vxfa_status_str.argtypes = [ctypes.c_int]
     L.vxfa_status_str.restype = ctypes.c_char_p
     L.vxfa_last_error.argtypes = [ctypes.c_void_p]
@@ -181,6 +199,16 @@ class Context:
         rc = self._lib.vxfa_flash_attn_ext_append(self._h, _ref(q), _ref(k), _ref(v), _ref(k_new), _ref(v_new),
                                                   _ref(mask), _ref(dst), scale, max_bias, logit_softcap,
                                                   ctypes.c_void_p(stream))
+        if check and rc != OK:
+            raise VxfaError(rc, self.last_error())
+        return rc
+
+    def flash_attn_ext_ring(self, q, k, v, ring_desc, k_new, v_new, dst, scale: float, max_bias: float = 0.0,
+                            logit_softcap: float = 0.0, stream: int = 0, check: bool = True) -> int:
+        """A decode step over a ring-buffer cache (k_new / v_new: the step's new row, or None)."""
+        rc = self._lib.vxfa_flash_attn_ext_ring(self._h, _ref(q), _ref(k), _ref(v), _ref(ring_desc), _ref(k_new),
+                                                _ref(v_new), _ref(dst), scale, max_bias, logit_softcap,
+                                                ctypes.c_void_p(stream))
         if check and rc != OK:
             raise VxfaError(rc, self.last_error())
         return rc
