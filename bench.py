@@ -67,13 +67,15 @@ def randn(torch, shape, seed, sigma=1.0, dtype=None):
 class Layer:
     """Descriptors of one flash_attn_ext call plus the tensors behind them."""
 
-    def __init__(self, q, k, v, mask, dst, scale, keep, md=None, kn=None, vn=None, fused=True, ring=None):
+    def __init__(self, q, k, v, mask, dst, scale, keep, md=None, kn=None, vn=None, fused=True, ring=None,
+                 rope=None):
         self.q, self.k, self.v, self.mask, self.dst = q, k, v, mask, dst
         self.scale = scale
         self.keep = keep
         self.md = md   # vxfa_mask_desc for the implicit-mask entry point, else None
         self.kn, self.vn, self.fused = kn, vn, fused   # new K/V rows (F32) to append first, else None
         self.ring = ring   # vxfa_ring: k/v are a ring-buffer cache
+        self.rope = rope   # vxfa_rope: rotate q and the appended K rows first
 
 
 def f32s(x):
@@ -159,6 +161,9 @@ def time_calls(torch, ctx, calls, steps, warmup, graph=True):
 
     def one_step(sh):
         for L in calls:
+            if L.rope is not None:   # rotary embedding + append + attention
+                ctx.flash_attn_ext_rope(L.q, L.k, L.v, L.kn, L.vn, L.rope, L.mask, L.dst, L.scale, stream=sh)
+                continue
             if L.ring is not None:   # decode step over a ring-buffer cache (+ its new row)
                 ctx.flash_attn_ext_ring(L.q, L.k, L.v, L.ring, L.kn, L.vn, L.dst, L.scale, stream=sh)
                 continue
@@ -343,10 +348,19 @@ def main():
                     calls = [Layer(L.q, L.k, L.v, None, L.dst, L.scale, L.keep, None, row(kn), row(vn), fused)
                              for L, (kn, vn) in zip(dl, news)]
                     _, res_app[fused] = time_calls(torch, ctx, calls, K, W)
+                # and with the rotary embedding of q and the new K row fused in (position 8191, theta 1e6)
+                pos = torch.full((1,), 8191, dtype=torch.int32, device="cuda")
+                rp = vxfa.rope(pos.data_ptr(), 128, 1.0e6)
+                calls = [Layer(L.q, L.k, L.v, None, L.dst, L.scale, L.keep, None, row(kn), row(vn), True, None, rp)
+                         for L, (kn, vn) in zip(dl, news)]
+                _, us_rope = time_calls(torch, ctx, calls, K, W)
                 log(f"[decode n_kv=8192 + append] fused {res_app[True]:.2f} us/layer; "
-                    f"append launch + attention {res_app[False]:.2f} us/layer")
+                    f"append launch + attention {res_app[False]:.2f} us/layer; "
+                    f"rope + append + attention fused {us_rope:.2f} us/layer")
                 configs["decode_nkv8192"].update({"append_fused_us_per_layer": res_app[True],
-                                                  "append_separate_us_per_layer": res_app[False]})
+                                                  "append_separate_us_per_layer": res_app[False],
+                                                  "rope_append_fused_us_per_layer": us_rope})
+                del pos
                 del news
             del dl
             torch.cuda.empty_cache()

@@ -206,6 +206,40 @@ int vxfa_flash_attn_ext_ring(vxfa_ctx* ctx, const vxfa_tensor* q,
                              float scale, float max_bias, float logit_softcap,
                              void* stream);
 
+/* Rotary embedding fused into the op. build_decoder_layer rotates Q and K
+ * with ggml_rope_ext (src/voxtral.cpp:1746-1749: mode 0, n_dims = head dim,
+ * freq_base = the decoder's rope theta, freq_scale 1, ext_factor 0,
+ * attn_factor 1), copies them contiguous (:1752-1753), stores K and V in
+ * the cache (:1758-1770) and attends (:1802); the realtime encoder rotates
+ * Q and K the same way with its own theta (:1595-1598). Pair j = dims
+ * (2j, 2j+1) of a head at position p turns by theta_j, theta_0 = p and
+ * theta_{j+1} = theta_j * freq_base^(-2 / n_dims) (ggml's running product),
+ * x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos; dims >= n_dims are not
+ * rotated. */
+typedef struct vxfa_rope {
+    const int32_t* positions;  /* device; token i of batch b: positions[b * Nq + i] */
+    int32_t n_dims;            /* rotated leading dims of each head (even, <= D)      */
+    int32_t mode;              /* 0 (ggml's GGML_ROPE_TYPE_NORMAL: adjacent pairs)    */
+    float   freq_base;         /* rope theta                                          */
+    float   freq_scale;        /* 1                                                   */
+} vxfa_rope;
+
+/* The op on unrotated inputs: rotate q (F32 [D, Nq, Hq, B]) and the new K
+ * rows, append the new rows (k_new, v_new F32 [Hkv * D, Nq, 1, B]: the new
+ * rows are the query tokens, at the last Nq rows of the F16 views k, v),
+ * then attend. Equals vxfa_flash_attn_ext_append(rope(q), k, v, rope(k_new),
+ * v_new, mask, ...) within the rounding of cos / sin. A decode step is one
+ * launch; otherwise the append (with K rotation) runs first. No counterpart
+ * in ggml's op: it replaces the two rope nodes, their contiguous copies, the
+ * two cache copies and the attention node of a layer. */
+int vxfa_flash_attn_ext_rope(vxfa_ctx* ctx, const vxfa_tensor* q,
+                             vxfa_tensor* k, vxfa_tensor* v,
+                             const vxfa_tensor* k_new,
+                             const vxfa_tensor* v_new, const vxfa_rope* rope,
+                             const vxfa_tensor* mask, vxfa_tensor* dst,
+                             float scale, float max_bias, float logit_softcap,
+                             void* stream);
+
 /* Human-readable name of a status code (static storage). */
 const char* vxfa_status_str(int status);
 

@@ -196,6 +196,38 @@ def ring_case(c: Case, capacity: int, start: int, seed=0) -> Case:
     return r
 
 
+def _powf(x, y):
+    """libm's powf, the function ggml's CPU rope uses for its theta scale."""
+    import ctypes
+    import ctypes.util
+    m = ctypes.CDLL(ctypes.util.find_library("m"))
+    m.powf.restype = ctypes.c_float
+    m.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    return np.float32(m.powf(np.float32(x), np.float32(y)))
+
+
+def rope_ggml(x, positions, n_dims, freq_base):
+    """ggml_rope_ext, mode 0, freq_scale 1, ext_factor 0, attn_factor 1 (the
+    arguments of src/voxtral.cpp:1746-1749): x [..., n_tok, heads, D] float32,
+    token t at positions[t]. Pair j of a head turns by theta_j with
+    theta_0 = p and theta_{j+1} = theta_j * powf(freq_base, -2 / n_dims) in
+    float32 (ggml's running product); cos / sin of the float32 angle."""
+    x = np.asarray(x, dtype=np.float32)
+    ts = _powf(freq_base, np.float32(-2.0) / np.float32(n_dims))
+    out = x.copy()
+    for t, p in enumerate(positions):
+        th = np.float32(p)
+        for j in range(n_dims // 2):
+            c = np.float32(np.cos(np.float64(th)))
+            s = np.float32(np.sin(np.float64(th)))
+            x0 = x[..., t, :, 2 * j]
+            x1 = x[..., t, :, 2 * j + 1]
+            out[..., t, :, 2 * j] = x0 * c - x1 * s
+            out[..., t, :, 2 * j + 1] = x0 * s + x1 * c
+            th = np.float32(th * ts)
+    return out
+
+
 def batched_case(n_streams=32, hq=32, hkv=8, hd=128, capacity=8192, lo=512, hi=8192, seed=5,
                  kv_sigma=0.5, name=None):
     """32 independent decode streams along ne[3] with ragged valid lengths

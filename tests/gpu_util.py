@@ -133,6 +133,35 @@ class Runner:
         after = {name: t.cpu().numpy() for name, t in dev.items()}
         return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy(), after
 
+    def run_rope(self, case, k_new, v_new, positions, n_dims, freq_base, mode=0, check=True):
+        """vxfa_flash_attn_ext_rope: rotate the case's q and k_new (F32
+        [Bk, n_new, Hkv * D]) at `positions` (int32 [B * Nq]), append, attend.
+        Returns (rc, out, device buffers after the call)."""
+        dev = to_device(case)
+        d = descs(case, dev)
+        kn = torch.from_numpy(np.ascontiguousarray(k_new, dtype=np.float32)).to("cuda")
+        vn = torch.from_numpy(np.ascontiguousarray(v_new, dtype=np.float32)).to("cuda")
+        pos = torch.from_numpy(np.ascontiguousarray(positions, dtype=np.int32)).to("cuda")
+        bk, n_new, row = k_new.shape
+        ne, nb = (row, n_new, 1, bk), (4, 4 * row, 4 * row * n_new, 4 * row * n_new)
+        dkn = vxfa.desc(kn.data_ptr(), vxfa.F32, ne, nb)
+        dvn = vxfa.desc(vn.data_ptr(), vxfa.F32, ne, nb)
+        rp = vxfa.rope(pos.data_ptr(), n_dims, freq_base, mode)
+        B, Nq, Hq, D = case.out_shape
+        n = B * Nq * Hq * D
+        buf = torch.from_numpy(np.full(n + 2 * CANARY, CANARY_BITS, dtype=np.uint32)).to("cuda")
+        dne, dnb = case.dst_ne_nb()
+        dst = vxfa.desc(buf.data_ptr() + 4 * CANARY, vxfa.F32, dne, dnb)
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = self.ctx.flash_attn_ext_rope(d["q"], d["k"], d["v"], dkn, dvn, rp, d.get("mask"), dst, case.scale,
+                                          stream=stream, check=check)
+        torch.cuda.synchronize()
+        host = buf.cpu().numpy()
+        assert (host[:CANARY] == CANARY_BITS).all(), "write before dst"
+        assert (host[CANARY + n:] == CANARY_BITS).all(), "write after dst"
+        after = {name: t.cpu().numpy() for name, t in dev.items()}
+        return rc, host[CANARY:CANARY + n].view(np.float32).reshape(B, Nq, Hq, D).copy(), after
+
     def close(self):
         self.ctx.close()
 

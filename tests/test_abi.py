@@ -189,3 +189,28 @@ def test_ring_struct_and_null_context():
     r = vxfa.ring(0, 1)
     assert lib.vxfa_flash_attn_ext_ring(None, None, None, None, ctypes.byref(r), None, None, None,
                                         0.1, 0.0, 0.0, None) == vxfa.INVALID_ARG
+
+
+def test_rope_struct_and_null_context():
+    # const int32_t* positions; int32 n_dims; int32 mode; float freq_base; float freq_scale
+    assert ctypes.sizeof(vxfa.VxfaRope) == 24 and vxfa.VxfaRope.freq_base.offset == 16
+    lib = vxfa.load()
+    r = vxfa.rope(0, 128, 1e6)
+    assert lib.vxfa_flash_attn_ext_rope(None, None, None, None, None, None, ctypes.byref(r), None, None,
+                                        0.1, 0.0, 0.0, None) == vxfa.INVALID_ARG
+
+
+def test_rope_restatement_closed_forms():
+    """Position 0 leaves vectors unchanged; one pair at position p turns by p
+    radians (theta_0 = p); the rotation keeps each pair's norm."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 2, 8)).astype(np.float32)
+    y = cases.rope_ggml(x, [0, 1, 7], 8, 10000.0)
+    assert np.array_equal(y[0], x[0])
+    c, s = np.cos(1.0), np.sin(1.0)
+    assert np.allclose(y[1, :, 0], x[1, :, 0] * c - x[1, :, 1] * s, atol=1e-6)
+    n0 = np.hypot(x[..., 0::2], x[..., 1::2])
+    n1 = np.hypot(y[..., 0::2], y[..., 1::2])
+    assert np.allclose(n0, n1, rtol=1e-5)
+    ts = cases._powf(10000.0, np.float32(-2.0) / np.float32(8))
+    assert abs(float(ts) - 10000.0 ** (-0.25)) < 1e-7

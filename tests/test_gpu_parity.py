@@ -578,3 +578,76 @@ def test_ring_rejects_bad_descriptors(runner):
     p.views["q"] = cases.prefill_case(4, seed=79, causal=False).views["q"]
     p.bufs["q"] = cases.prefill_case(4, seed=79, causal=False).bufs["q"]
     assert runner.run_ring(p, vx.ring(5, 100), check=False)[0] == vx.UNSUPPORTED
+
+
+# --- rotary embedding fused into the op: vxfa_flash_attn_ext_rope -------------
+# The same call with q and the new K rows rotated on the host by the ggml
+# restatement (cases.rope_ggml) and passed through vxfa_flash_attn_ext_append
+# is the reference; cos / sin may differ in the last bit between the device
+# and the host, so outputs are compared at 2e-4 and cache bytes to within one
+# f16 step (and mostly equal), besides the oracle bar.
+
+def _rope_check(runner, c, k_new, v_new, positions, n_dims, base):
+    import copy
+    import gpu_util
+    B, Nq, Hq, D = c.out_shape
+    qb, qt, qne, qnb, qoff = c.views["q"]
+    q = c.bufs[qb]
+    # q buffers are [B][tokens][heads][D] (the mul_mat output's view); rotate per token
+    q4 = q.reshape(B, -1, Hq, D)
+    pos_b = np.asarray(positions, dtype=np.int32).reshape(B, Nq)
+    qr = np.stack([cases.rope_ggml(q4[b], pos_b[b], n_dims, base) for b in range(B)]).reshape(q.shape)
+    hkv = k_new.shape[2] // D
+    kr = np.stack([cases.rope_ggml(k_new[b].reshape(Nq, hkv, D), pos_b[b], n_dims, base).reshape(Nq, -1)
+                   for b in range(k_new.shape[0])])
+    host = copy.deepcopy(c)
+    host.bufs[qb] = qr.astype(np.float32)
+    _say(f"[rope] {c.name} n_dims={n_dims} base={base} positions {positions[0]}..{positions[-1]}")
+    rc, ref, _ = runner.run_append(host, kr, v_new, fused=True)
+    assert rc == 0
+    rc, out, after = runner.run_rope(c, k_new, v_new, positions, n_dims, base)
+    assert rc == 0
+    m, r, ok = gpu_util.parity(out, ref, 2e-4, 2e-4)
+    _say(f"    vs host-rotated maxabs={m:.3e} rel={r:.3e}")
+    assert ok, (m, r)
+    e = _expected_cache(host, kr, v_new)
+    for role in ("k", "v"):
+        b = c.views[role][0]
+        got = after[b].view(np.uint16).astype(np.int32)
+        want = e.bufs[b].view(np.uint16).reshape(-1).astype(np.int32)
+        diff = np.abs(got - want)
+        _say(f"    {role} cache: {int((diff > 0).sum())} of {diff.size} halves differ, max {int(diff.max())} steps")
+        assert diff.max() <= 1 and (diff > 0).mean() < 1e-3
+    exact = cases.oracle_f64(e)
+    m, r, ok = gpu_util.parity(out, exact, ATOL, RTOL)
+    assert ok, (m, r)
+
+
+def test_rope_decode_step(runner):
+    """Decoder step at position 8191 (theta 1e6, hd 128): q and the new row rotated."""
+    c = cases.decode_case(8192, capacity=8192, seed=81)
+    k_new, v_new = _append_rows(np.random.default_rng(81), 1, 1, 8 * 128)
+    _rope_check(runner, c, k_new, v_new, [8191], 128, 1.0e6)
+
+
+def test_rope_prefill_after_cache(runner):
+    c = cases.prefill_case(64, seed=82, kv_offset=448)
+    k_new, v_new = _append_rows(np.random.default_rng(82), 1, 64, 8 * 128)
+    _rope_check(runner, c, k_new, v_new, list(range(448, 512)), 128, 1.0e6)
+
+
+def test_rope_partial_dims_and_small_base(runner):
+    c = cases.prefill_case(40, hq=8, hkv=2, hd=64, seed=83, kv_offset=10)
+    k_new, v_new = _append_rows(np.random.default_rng(83), 1, 40, 2 * 64)
+    _rope_check(runner, c, k_new, v_new, list(range(1000, 1040)), 48, 10000.0)
+
+
+def test_rope_rejects_unsupported(runner):
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.decode_case(64, seed=84)
+    k_new, v_new = _append_rows(np.random.default_rng(84), 1, 1, 8 * 128)
+    assert runner.run_rope(c, k_new, v_new, [63], 128, 1e6, mode=2, check=False)[0] == vx.UNSUPPORTED
+    assert runner.run_rope(c, k_new, v_new, [63], 127, 1e6, check=False)[0] == vx.INVALID_ARG
+    k2, v2 = _append_rows(np.random.default_rng(84), 1, 2, 8 * 128)
+    assert runner.run_rope(c, k2, v2, [62, 63], 128, 1e6, check=False)[0] == vx.INVALID_ARG

@@ -51,6 +51,12 @@ struct AttnArgs {
     // decode over a ring buffer: logical position p is cache row
     // (ring_start + p) mod ring_cap; 0, 0 = a plain cache
     int32_t ring_start, ring_cap;
+    // rotary embedding of Q (and of the appended K rows), ggml's mode 0:
+    // position of query row i of batch b at rope_pos[b * nq + i]; rope_pos
+    // null = no rotation
+    const int32_t* rope_pos;
+    float rope_ts;        // theta scale = freq_base^(-2 / n_dims)
+    int32_t rope_dims;    // rotated leading dims of each head
     const float* k_new;
     const float* v_new;
     int64_t kn_nb3, vn_nb3;
@@ -66,7 +72,70 @@ struct AppendArgs {
     _Float16* v;
     int64_t k_nb1, k_nb2, k_nb3, v_nb1, v_nb2, v_nb3;
     int32_t d, hkv, n_new, pos0, bk;   // rows pos0 .. pos0 + n_new - 1 are written
+    // K rows rotated first (mode 0) at position rope_pos[b * n_new + t]; null = none
+    const int32_t* rope_pos;
+    float rope_ts;
+    int32_t rope_dims;
 };
+
+// Rotary embedding as ggml_rope_ext computes it for mode 0 with
+// freq_scale 1, ext_factor 0, attn_factor 1 (the arguments voxtral.cpp
+// passes at src/voxtral.cpp:1746-1749 and :1595-1598): pair j = (x[2j],
+// x[2j+1]) of a head turns by theta_j, where theta_0 = p and each next
+// pair's angle is the previous one times ts = freq_base^(-2 / n_dims), in
+// that order (ggml builds its cos/sin cache by this running product), and
+// x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos. x holds dims d0 .. d0 + 7
+// (d0 even); dims at or past n_dims are left as they are. cos and sin are
+// taken of the angle reduced modulo 2 pi in double precision and rounded to
+// float (within a float ulp of the unreduced angle's cosf / sinf).
+// cos / sin of pair j's angle at position p (see rope8 below): the running
+// product to pair j, reduced modulo 2 pi in double precision (error ~1e-12)
+// so sincosf takes its short-argument path, rounded to float.
+__device__ __forceinline__ float2 rope_cs(int p, int j, float ts) {
+    float th = (float)p;
+    for (int i = 0; i < j; ++i) th *= ts;
+    const double td = (double)th;
+    const double kq = __builtin_rint(td * 0.15915494309189535);
+    const float r = (float)__builtin_fma(-kq, 6.283185307179586, td);
+    float s, c;
+    sincosf(r, &s, &c);
+    return float2{c, s};
+}
+
+// rope8 with the pairs' cos / sin taken from a table: cs[j] = rope_cs(p, j, ts).
+__device__ __forceinline__ void rope8_tab(float (&x)[8], int d0, const float2* cs, int n_dims) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (d0 + 2 * k < n_dims) {
+            const float2 t = cs[d0 / 2 + k];
+            const float x0 = x[2 * k], x1 = x[2 * k + 1];
+            x[2 * k] = x0 * t.x - x1 * t.y;
+            x[2 * k + 1] = x0 * t.y + x1 * t.x;
+        }
+    }
+}
+
+__device__ __forceinline__ void rope8(float (&x)[8], int p, int d0, float ts, int n_dims) {
+    if (d0 >= n_dims) return;
+    float th = (float)p;
+    for (int j = 0; j < d0 / 2; ++j) th *= ts;   // the running product up to pair d0 / 2
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (d0 + 2 * k < n_dims) {
+            // angles reach n_ctx radians: reduce by 2 pi in double first (error
+            // ~1e-12), then sincosf's short-argument path applies
+            const double td = (double)th;
+            const double kq = __builtin_rint(td * 0.15915494309189535);
+            const float r = (float)__builtin_fma(-kq, 6.283185307179586, td);
+            float s, c;
+            sincosf(r, &s, &c);
+            const float x0 = x[2 * k], x1 = x[2 * k + 1];
+            x[2 * k] = x0 * c - x1 * s;
+            x[2 * k + 1] = x0 * s + x1 * c;
+        }
+        th *= ts;
+    }
+}
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

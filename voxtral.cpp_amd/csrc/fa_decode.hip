@@ -66,6 +66,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     __shared__ float lds_l[DEC_WAVES][G];
     __shared__ int lds_red[2 * DEC_WAVES];
     __shared__ half8 lds_q[G * D / 8];   // the group's query heads, f16, [G][D]
+    __shared__ float2 lds_rope[D / 2];   // cos / sin of each pair's rotary angle (with rope_pos)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -75,6 +76,21 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     const int b = blockIdx.y;
     const int bkv = b / (a.b / a.bk);
     constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
+    // rotary position of the query token (also the appended row's: the host
+    // requires one kv batch per q batch), requested before any other load. A
+    // vector load (the opaque zero offset keeps it off the scalar unit, whose
+    // out-of-order returns would make the first wait for kernel arguments
+    // wait for it too); the in-order vector count then waits for it alone.
+    // The load is unconditional (without rotary positions it reads a word of
+    // the K cache and ignores it): a branch around it would keep the wait
+    // for it next to it.
+    int rope_p;
+    {
+        const int32_t* rp = a.rope_pos ? a.rope_pos + b : reinterpret_cast<const int32_t*>(a.k);
+        int z;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+        rope_p = rp[z];
+    }
 
     // ---- live range of the KV axis -------------------------------------
     // The mask rows of this group's query heads: planes (g G + j) % hm of
@@ -143,7 +159,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         const int pend = min(p0 + DEC_TILE, hi_main);
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
-            const int pos = min(p0 + 16 * grp + (lane & 15), pend - 1);
+            const int pos = max(min(p0 + 16 * grp + (lane & 15), pend - 1), 0);
             const char* kp = kb + (int64_t)row_of(pos) * a.k_nb1 + kcol * 2;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
@@ -154,7 +170,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int pos = min(p0 + vrow + i * RPI, pend - 1);
+            const int pos = max(min(p0 + vrow + i * RPI, pend - 1), 0);
             T.v[i] = *(const half8*)(vb + (int64_t)row_of(pos) * a.v_nb1 + vcol * 2);
         }
     };
@@ -180,19 +196,33 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
 #pragma unroll
         for (int u = 0; u < QCH; ++u) qraw[u] = p[u];
     }
+    // The first tile's loads are unconditional (a wavefront without a tile
+    // reads a clamped row it never uses): straight-line code lets the
+    // compiler count the loads in flight exactly at the waits that follow.
     Tile TA, TB;
     int t = t_begin + wave;
-    if (t < t_end) load_tile(TA, t);
+    load_tile(TA, t < t_end ? t : t_begin);
+    // the rotary cos / sin table, by wavefront 0 while the tile loads are in
+    // flight; the q_loader lanes read it next, in program order. (The empty
+    // asm takes the position as an operand after those loads are issued, so
+    // the wait for it stays below them.)
+    asm volatile("" : "+v"(rope_p) : : "memory");
+    if (a.rope_pos && tid < D / 2) lds_rope[tid] = rope_cs(rope_p, tid, a.rope_ts);
     if (q_loader) {
         half8 qh8;
         if constexpr (QF16) {
             qh8 = __builtin_bit_cast(half8, qraw[0]);
         } else {
+            float x[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                qh8[e] = (_Float16)qraw[0][e];
-                qh8[4 + e] = (_Float16)qraw[QCH - 1][e];
+                x[e] = qraw[0][e];
+                x[4 + e] = qraw[QCH - 1][e];
             }
+            // rotary embedding of the query (position of batch b's token)
+            if (a.rope_pos) rope8_tab(x, 8 * (tid % (D / 8)), lds_rope, a.rope_dims);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qh8[e] = (_Float16)x[e];
         }
         lds_q[tid] = qh8;
     }
@@ -291,23 +321,32 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         const int pn = a.nkv - 1;
         const float* kn = (const float*)((const char*)a.k_new + (int64_t)bkv * a.kn_nb3) + g * D;
         const float* vn = (const float*)((const char*)a.v_new + (int64_t)bkv * a.vn_nb3) + g * D;
-        auto cvt8 = [](const float* p) {
-            const floatx4 x0 = *(const floatx4*)p, x1 = *(const floatx4*)(p + 4);
-            half8 y;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                y[i] = (_Float16)x0[i];
-                y[4 + i] = (_Float16)x1[i];
-            }
-            return y;
-        };
+        // every load of the row first (one round trip), then rotation (K, with
+        // rope_pos; the table holds the row's angles) and rounding
+        floatx4 kr[KS][2], vr[2];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const half8 kx = cvt8(kn + kcol + 32 * ks);
+            kr[ks][0] = *(const floatx4*)(kn + kcol + 32 * ks);
+            kr[ks][1] = *(const floatx4*)(kn + kcol + 32 * ks + 4);
+        }
+        vr[0] = *(const floatx4*)(vn + vcol);
+        vr[1] = *(const floatx4*)(vn + vcol + 4);
+        auto cvt8 = [&](const floatx4 (&r)[2], int d0, bool rot) {
+            float x[8] = {r[0][0], r[0][1], r[0][2], r[0][3], r[1][0], r[1][1], r[1][2], r[1][3]};
+            if (rot) rope8_tab(x, d0, lds_rope, a.rope_dims);
+            half8 y;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = (_Float16)x[i];
+            return y;
+        };
+        const bool rot = a.rope_pos != nullptr;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 kx = cvt8(kr[ks], kcol + 32 * ks, rot);
             TA.k[0][ks] = kx;
             TA.k[1][ks] = kx;
         }
-        const half8 vx = cvt8(vn + vcol);
+        const half8 vx = cvt8(vr, vcol, false);
 #pragma unroll
         for (int i = 0; i < NV; ++i) TA.v[i] = vx;
         if constexpr (masked) {

@@ -8,6 +8,9 @@
 // thread converts 8 consecutive elements (two 16-byte loads, one 16-byte
 // store). The source row is Hkv * D floats, kv head h at h * D (the layout of
 // the reshape at :1743); the cache row of head h is the view's (pos, h) row.
+// With rope_pos set, K rows are first turned by the rotary embedding of
+// their token's position (ggml_rope_ext mode 0, :1748-1749), as the
+// reference rotates K before storing it.
 #include "fa_common.h"
 
 namespace vxfa {
@@ -15,6 +18,13 @@ namespace vxfa {
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
     const int t = blockIdx.x, b = blockIdx.y;
     const int per = a.hkv * a.d / 8;   // 8-element chunks per matrix row
+    // the token's rotary cos / sin per pair, shared by its kv heads
+    __shared__ float2 cs[128];
+    if (a.rope_pos) {
+        const int p = a.rope_pos[b * a.n_new + t];
+        for (int j = threadIdx.x; j < a.d / 2; j += 256) cs[j] = rope_cs(p, j, a.rope_ts);
+        __syncthreads();
+    }
     for (int c = threadIdx.x; c < 2 * per; c += 256) {
         const bool is_v = c >= per;
         const int e = 8 * (is_v ? c - per : c);
@@ -23,12 +33,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
         const int64_t soff = (int64_t)t * (is_v ? a.vn_nb1 : a.kn_nb1) + (int64_t)b * (is_v ? a.vn_nb3 : a.kn_nb3);
         const floatx4* sp = (const floatx4*)((const char*)src + soff) + e / 4;
         const floatx4 x0 = sp[0], x1 = sp[1];
+        float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        if (!is_v && a.rope_pos) rope8_tab(x, d, cs, a.rope_dims);
         half8 y;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            y[i] = (_Float16)x0[i];
-            y[4 + i] = (_Float16)x1[i];
-        }
+        for (int i = 0; i < 8; ++i) y[i] = (_Float16)x[i];
         const int64_t pos = (int64_t)a.pos0 + t;
         char* dst = is_v ? (char*)a.v + pos * a.v_nb1 + (int64_t)h * a.v_nb2 + (int64_t)b * a.v_nb3
                          : (char*)a.k + pos * a.k_nb1 + (int64_t)h * a.k_nb2 + (int64_t)b * a.k_nb3;
@@ -38,7 +47,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
 
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t st) {
     if (a.n_new <= 0 || a.bk <= 0) return hipSuccess;
-    if (a.d % 8 || a.bk > 65535) return hipErrorInvalidValue;
+    if (a.d % 8 || a.d > 256 || a.bk > 65535) return hipErrorInvalidValue;
     hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)a.n_new, (unsigned)a.bk), dim3(256), 0, st, a);
     return hipGetLastError();
 }

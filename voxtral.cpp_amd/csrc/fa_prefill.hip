@@ -231,7 +231,19 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         const int64_t qoff = (int64_t)(qvalid ? qrow : 0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const half8 v = load_q8(a.q, qoff + (int64_t)(16 * ks + 8 * hh) * qelt, QF16);
+            half8 v;
+            if (!QF16 && a.rope_pos) {
+                // rotary embedding of the query row (position of row qrow of batch b)
+                const floatx4* p = (const floatx4*)((const char*)a.q + qoff + (int64_t)(16 * ks + 8 * hh) * 4);
+                const floatx4 x0 = p[0], x1 = p[1];
+                float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                rope8(x, a.rope_pos[(int64_t)b * a.nq + (qvalid ? qrow : 0)], 16 * ks + 8 * hh, a.rope_ts,
+                      a.rope_dims);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (_Float16)x[e];
+            } else {
+                v = load_q8(a.q, qoff + (int64_t)(16 * ks + 8 * hh) * qelt, QF16);
+            }
             qb[ks] = qvalid ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }

@@ -259,12 +259,29 @@ namespace {
 // enforce it).
 int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
         const vxfa_mask_desc* im, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream,
-        const vxfa_tensor* k_new = nullptr, const vxfa_tensor* v_new = nullptr, const vxfa_ring* ring = nullptr) {
+        const vxfa_tensor* k_new = nullptr, const vxfa_tensor* v_new = nullptr, const vxfa_ring* ring = nullptr,
+        const vxfa_rope* rope = nullptr) {
     if (!c) return VXFA_INVALID_ARG;
     c->last_error[0] = 0;
     const char* why = nullptr;
     int rc = check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
     if (rc == VXFA_OK && k_new) rc = check_append(k, v, k_new, v_new, &why);
+    if (rc == VXFA_OK && rope) {
+        if (!rope->positions || !k_new) {
+            why = "rope: positions and the new K/V rows are required";
+            rc = VXFA_INVALID_ARG;
+        } else if (k_new->ne[1] != q->ne[1] || q->ne[3] != k->ne[3]) {
+            why = "rope: the new rows are the query tokens (n_new = Nq, one kv batch per q batch)";
+            rc = VXFA_INVALID_ARG;
+        } else if (rope->n_dims <= 0 || rope->n_dims % 2 || rope->n_dims > q->ne[0]) {
+            why = "rope: n_dims must be even and at most the head dim";
+            rc = VXFA_INVALID_ARG;
+        } else if (rope->mode != 0 || rope->freq_scale != 1.0f || !(rope->freq_base > 0.0f) ||
+                   q->type != VXFA_TYPE_F32) {
+            why = "rope: mode 0, freq_scale 1, freq_base > 0 and F32 q only";
+            rc = VXFA_UNSUPPORTED;
+        }
+    }
     if (rc == VXFA_OK && ring) {
         const int64_t G = q->ne[2] / k->ne[2];
         if (ring->start < 0 || ring->start >= k->ne[1] || ring->n_kv < 0 || ring->n_kv > k->ne[1]) {
@@ -294,8 +311,16 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     hipError_t e = hipSetDevice(c->device);
     if (e != hipSuccess) { set_err(c, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // rotary embedding: ggml's theta scale, computed as ggml_rope_ext's CPU path does
+    const float rope_ts = rope ? powf(rope->freq_base, -2.0f / (float)rope->n_dims) : 0.0f;
     if (append && !fuse_append) {
-        e = vxfa::launch_kv_append(append_args(k, v, k_new, v_new), st);
+        vxfa::AppendArgs ap = append_args(k, v, k_new, v_new);
+        if (rope) {
+            ap.rope_pos = rope->positions;
+            ap.rope_ts = rope_ts;
+            ap.rope_dims = rope->n_dims;
+        }
+        e = vxfa::launch_kv_append(ap, st);
         if (e != hipSuccess) { set_err(c, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     }
     if (Nq * Hq * B == 0) return VXFA_OK;
@@ -330,6 +355,11 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     if (ring) {
         a.ring_start = (int32_t)ring->start;
         a.ring_cap = (int32_t)k->ne[1];
+    }
+    if (rope) {
+        a.rope_pos = rope->positions;
+        a.rope_ts = rope_ts;
+        a.rope_dims = rope->n_dims;
     }
     if (fuse_append) {
         a.append = 1;
@@ -381,7 +411,7 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
             a.ws = c->ws;
         }
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
-    } else if (D == 64 && !mask && !implicit && scale != 0.0f && c->pp_enabled) {
+    } else if (D == 64 && !mask && !implicit && !rope && scale != 0.0f && c->pp_enabled) {
         // (scale 0 goes to the general kernel: the pipelined one folds the
         // scale into the exponent and scores the partial block's dead rows -inf)
         // encoder prefill: the software-pipelined hd 64 kernel
@@ -452,6 +482,19 @@ int vxfa_flash_attn_ext_ring(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, 
         return VXFA_INVALID_ARG;
     }
     return run(c, q, k, v, nullptr, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, ring);
+}
+
+int vxfa_flash_attn_ext_rope(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, vxfa_tensor* v,
+                             const vxfa_tensor* k_new, const vxfa_tensor* v_new, const vxfa_rope* rope,
+                             const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias,
+                             float logit_softcap, void* stream) {
+    if (!c) return VXFA_INVALID_ARG;
+    if (!rope || !k_new || !v_new) {
+        c->last_error[0] = 0;
+        set_err(c, "rope, k_new and v_new are required");
+        return VXFA_INVALID_ARG;
+    }
+    return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, nullptr, rope);
 }
 
 int vxfa_check_mask_desc(const vxfa_mask_desc* m) {

@@ -30,6 +30,7 @@ EXPORTS = (
     "vxfa_kv_append",
     "vxfa_flash_attn_ext_append",
     "vxfa_flash_attn_ext_ring",
+    "vxfa_flash_attn_ext_rope",
     "vxfa_status_str",
     "vxfa_last_error",
     "vxfa_version",
@@ -76,6 +77,23 @@ def ring(start: int, n_kv: int) -> VxfaRing:
     return r
 
 
+class VxfaRope(ctypes.Structure):
+    """vxfa_rope: ggml_rope_ext mode 0 with freq_scale 1 (positions: device int32 pointer)."""
+    _fields_ = [
+        ("positions", ctypes.c_void_p),
+        ("n_dims", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("freq_base", ctypes.c_float),
+        ("freq_scale", ctypes.c_float),
+    ]
+
+
+def rope(positions_ptr: int, n_dims: int, freq_base: float, mode: int = 0, freq_scale: float = 1.0) -> VxfaRope:
+    r = VxfaRope()
+    r.positions, r.n_dims, r.mode, r.freq_base, r.freq_scale = positions_ptr, n_dims, mode, freq_base, freq_scale
+    return r
+
+
 class VxfaError(RuntimeError):
     def __init__(self, status: int, msg: str):
         super().__init__(f"vxfa status {status} ({status_str(status)}): {msg}")
@@ -118,6 +136,9 @@ def load() -> ctypes.CDLL:
     L.vxfa_flash_attn_ext_ring.argtypes = [ctypes.c_void_p, P, P, P, ctypes.POINTER(VxfaRing), P, P, P,
                                            ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
     L.vxfa_flash_attn_ext_ring.restype = ctypes.c_int
+    L.vxfa_flash_attn_ext_rope.argtypes = [ctypes.c_void_p, P, P, P, P, P, ctypes.POINTER(VxfaRope), P, P,
+                                           ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
+    L.vxfa_flash_attn_ext_rope.restype = ctypes.c_int
     L.vxfa_status_str.argtypes = [ctypes.c_int]
     L.vxfa_status_str.restype = ctypes.c_char_p
     L.vxfa_last_error.argtypes = [ctypes.c_void_p]
@@ -209,6 +230,16 @@ class Context:
         rc = self._lib.vxfa_flash_attn_ext_ring(self._h, _ref(q), _ref(k), _ref(v), _ref(ring_desc), _ref(k_new),
                                                 _ref(v_new), _ref(dst), scale, max_bias, logit_softcap,
                                                 ctypes.c_void_p(stream))
+        if check and rc != OK:
+            raise VxfaError(rc, self.last_error())
+        return rc
+
+    def flash_attn_ext_rope(self, q, k, v, k_new, v_new, rope_desc, mask, dst, scale: float, max_bias: float = 0.0,
+                            logit_softcap: float = 0.0, stream: int = 0, check: bool = True) -> int:
+        """Rotate q and the new K rows (mode 0), append the new rows, attend."""
+        rc = self._lib.vxfa_flash_attn_ext_rope(self._h, _ref(q), _ref(k), _ref(v), _ref(k_new), _ref(v_new),
+                                                _ref(rope_desc), _ref(mask), _ref(dst), scale, max_bias,
+                                                logit_softcap, ctypes.c_void_p(stream))
         if check and rc != OK:
             raise VxfaError(rc, self.last_error())
         return rc
