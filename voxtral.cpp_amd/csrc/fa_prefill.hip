@@ -76,47 +76,96 @@ constexpr int PF_MAXT = 512;            // 64-position tiles classified per row 
 // selects the same KV steps as the exact range (steps are whole tiles).
 //
 // One wavefront takes one (group, tile) unit at a time, four units per
-// batch, all of a batch's loads issued before any is used. A unit's rows are
-// 128-byte segments at any 2-byte alignment (voxtral's n x n mask rows are 2n
-// bytes apart): nine lanes read one row's segment as the 16-byte-aligned
-// chunks that cover it, seven rows per load instruction, five instructions
-// per unit. Each chunk holds at least one byte of the row, so it lies in the
-// same 16-byte granule of the same allocation and page as mask data; entries
-// outside the segment are dropped in registers.
-template <int NT, int NG>
+// batch, all of a batch's loads issued before any is used and none under a
+// branch. A unit's rows are 128-byte segments at any 2-byte alignment
+// (voxtral's n x n mask rows are 2n bytes apart): nine lanes read one row's
+// segment as the 16-byte-aligned chunks that cover it, seven rows per load
+// instruction, five instructions per unit. Rows 32 apart share their
+// misalignment (the stride is even), so each lane sets up its five rows once:
+// their aligned start, their last chunk holding mask data, and which entries of
+// its chunk fall inside a full tile (all 8 but for the first and last chunk
+// of the segment). A chunk past a row's data is replaced by the row's last
+// one, and a lane without a row (or past the workgroup's rows) reads row 0,
+// so every chunk read holds mask data: it lies in the same 16-byte granule of
+// the same allocation and page. Entries outside the tile, or read in place of
+// another, are dropped in registers.
+__device__ __forceinline__ uint32_t half_mask(uint32_t m8, int j) {   // entries 2j, 2j+1 -> 16-bit halves
+    return (((m8 >> (2 * j)) & 1u) ? 0x0000FFFFu : 0u) | (((m8 >> (2 * j + 1)) & 1u) ? 0xFFFF0000u : 0u);
+}
+__device__ __forceinline__ uint32_t entry_range(int e_lo, int e_hi) {   // bits [e_lo, e_hi) of 8
+    return e_hi > e_lo ? (((1u << e_hi) - 1u) & ~((1u << e_lo) - 1u)) : 0u;
+}
+// A barrier that orders LDS accesses only: a full __syncthreads() would
+// also wait for every global load still in flight (here, the query rows).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// after_loads() runs once per wavefront right after its first batch's loads
+// are issued (before any is waited for): the caller issues its own loads
+// there, so the scan's wait does not include them (loads complete in order).
+template <int NT, int NG, class F>
 __device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t row_stride, int rows, int n,
-                                                uint8_t* flags, int* red, int& lo, int& hi) {
+                                                uint8_t* flags, int* red, int& lo, int& hi, F&& after_loads) {
     constexpr int NWV = NT / 64;
     constexpr int UB = 4;            // units per wavefront batch
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ntile_all = (n + 63) >> 6;
     const int ntile = min(ntile_all, PF_MAXT);
     const int units = NG * ntile;
     const int lr = lane / 9, lc = lane - 9 * lr;   // row in a batch of 7 (lane 63 idle), chunk 0..8
+    const int last_span = n - 64 * (ntile_all - 1);   // entries of the last tile
+    // (pointer arithmetic on const char*: integer addresses would make the
+    // compiler fall back to flat loads)
+    const char* b0 = reinterpret_cast<const char*>(base);
+    const int64_t gstride = 32 * row_stride;
+    // row 0 of the workgroup: the row read in place of a missing one
+    const int mis0 = (int)(reinterpret_cast<uintptr_t>(b0) & 15);
+    const char* rowa0 = b0 - mis0;
+    const int kmax0 = (2 * n - 1 + mis0) >> 4;
+    // this lane's row 7 bt + lr of group 0
+    const char* rowa[5];   // 16-byte-aligned start
+    int kmax[5];           // last chunk holding mask data
+    int mis2[5];           // misalignment in entries
+    uint32_t m8i[5];       // entries of the lane's chunk inside a full tile
+    uint32_t hmi[5][4];    // the same as 16-bit halves of the chunk's words
+#pragma unroll
+    for (int bt = 0; bt < 5; ++bt) {
+        const int rr = 7 * bt + lr;
+        const bool lane_row = lr < 7 && rr < 32;
+        const char* rp = b0 + (int64_t)(lane_row ? rr : 0) * row_stride;
+        const int mis = (int)(reinterpret_cast<uintptr_t>(rp) & 15);
+        rowa[bt] = rp - mis;
+        kmax[bt] = (2 * n - 1 + mis) >> 4;
+        mis2[bt] = mis >> 1;
+        m8i[bt] = lane_row ? entry_range(lc == 0 ? mis >> 1 : 0, lc == 8 ? mis >> 1 : 8) : 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hmi[bt][j] = half_mask(m8i[bt], j);
+    }
     int tlo = 0x7fffffff, thi = -1;                // live tiles (wave-uniform)
-    for (int ub = wave * UB; ub < units; ub += NWV * UB) {
+    // The first batch is straight-line code: at a loop's head the compiler
+    // would wait for the loads issued before the scan (Q) first.
+    auto batch = [&](int ub, bool first) {
         u32x4 w[UB][5];
-        int colc[UB][5];   // column of the chunk's first entry relative to the tile (may be < 0)
+        bool okr[UB][5];
 #pragma unroll
         for (int i = 0; i < UB; ++i) {
-            const int u = ub + i;
+            const int u = min(ub + i, units - 1);   // past the last unit: a repeat, unused
             const int g = u / ntile, t = u - g * ntile;
-            const int c0 = 64 * t, c1 = min(64 * t + 64, n);
 #pragma unroll
             for (int bt = 0; bt < 5; ++bt) {
                 const int rr = 7 * bt + lr;
-                const int row = 32 * g + rr;
-                const char* rowp = reinterpret_cast<const char*>(base) + (int64_t)row * row_stride;
-                const char* s0p = rowp + 2 * c0;
-                const int mis = (int)(reinterpret_cast<uintptr_t>(s0p) & 15);
-                const int off = 16 * lc - mis;               // chunk start relative to s0p, bytes
-                const bool ok = u < units && lr < 7 && rr < 32 && row < rows && off < 2 * (c1 - c0);
-                colc[i][bt] = ok ? off / 2 : 64;             // 64: no entry in the tile
-                w[i][bt] = u32x4{0u, 0u, 0u, 0u};
-                if (ok) w[i][bt] = *reinterpret_cast<const u32x4*>(s0p + off);
+                const bool ok = lr < 7 && rr < 32 && 32 * g + rr < rows;
+                const char* ra = ok ? rowa[bt] + (int64_t)g * gstride : rowa0;
+                const int k = min(8 * t + lc, ok ? kmax[bt] : kmax0);
+                okr[i][bt] = ok;
+                w[i][bt] = *reinterpret_cast<const u32x4*>(ra + 16 * k);
             }
         }
+        if (first) after_loads();
 #pragma unroll
         for (int i = 0; i < UB; ++i) {
             const int u = ub + i;
@@ -124,19 +173,30 @@ __device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t ro
             const int g = u / ntile, t = u - g * ntile;
             const int span = min(64 * t + 64, n) - 64 * t;
             uint32_t acc_l = 0, acc_n = 0;
-#pragma unroll
-            for (int bt = 0; bt < 5; ++bt) {
-                // entries [e_lo, e_hi) of the chunk lie in the tile's span
-                const int e_lo = min(max(-colc[i][bt], 0), 8);
-                const int e_hi = min(max(span - colc[i][bt], 0), 8);
-                const uint32_t m8 = e_hi > e_lo ? ((1u << (e_hi - e_lo)) - 1u) << e_lo : 0u;
+            // halves kept by hm: a half is not -inf when (w & hm) ^ (hm & -inf)
+            // is not zero there, not +-0 when w & hm & 0x7FFF is not
+            auto scan_chunk = [&](int bt, const uint32_t (&hm)[4]) {
+                uint32_t tl = 0, tn = 0;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t s0 = (uint32_t)(((int32_t)(m8 << (31 - 2 * j))) >> 31);
-                    const uint32_t s1 = (uint32_t)(((int32_t)(m8 << (30 - 2 * j))) >> 31);
-                    const uint32_t hm = (s0 & 0xFFFFu) | (s1 & 0xFFFF0000u);
-                    acc_l |= (w[i][bt][j] ^ 0xFC00FC00u) & hm;   // a half is not -inf
-                    acc_n |= (w[i][bt][j] & 0x7FFF7FFFu) & hm;   // a half is not +-0
+                    tl |= (w[i][bt][j] & hm[j]) ^ (hm[j] & 0xFC00FC00u);
+                    tn |= w[i][bt][j] & hm[j];
+                }
+                if (okr[i][bt]) {
+                    acc_l |= tl;
+                    acc_n |= tn & 0x7FFF7FFFu;
+                }
+            };
+            if (t != ntile_all - 1) {
+#pragma unroll
+                for (int bt = 0; bt < 5; ++bt) scan_chunk(bt, hmi[bt]);
+            } else {
+                // the last tile ends at n
+#pragma unroll
+                for (int bt = 0; bt < 5; ++bt) {
+                    const uint32_t m8 = m8i[bt] & entry_range(0, min(last_span - 8 * lc + mis2[bt], 8));
+                    const uint32_t hm[4] = {half_mask(m8, 0), half_mask(m8, 1), half_mask(m8, 2), half_mask(m8, 3)};
+                    scan_chunk(bt, hm);
                 }
             }
             const bool live = __any(acc_l != 0);
@@ -146,14 +206,17 @@ __device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t ro
             if (live) { tlo = min(tlo, t); thi = max(thi, t); }
             if (lane == 0) flags[g * PF_MAXT + t] = (uint8_t)bits;
         }
-    }
+    };
+    if (wave * UB < units) batch(wave * UB, true);
+    else after_loads();
+    for (int ub = wave * UB + NWV * UB; ub < units; ub += NWV * UB) batch(ub, false);
     if (lane == 0) { red[2 * wave] = tlo; red[2 * wave + 1] = thi; }
-    __syncthreads();
+    lds_barrier();
     tlo = red[0];
     thi = red[1];
 #pragma unroll
     for (int wv = 1; wv < NWV; ++wv) { tlo = min(tlo, red[2 * wv]); thi = max(thi, red[2 * wv + 1]); }
-    __syncthreads();   // red may be reused by the caller
+    lds_barrier();   // red may be reused by the caller
     if (ntile_all > PF_MAXT) {   // unclassified tail: keep it in the range
         tlo = min(tlo, PF_MAXT);
         thi = ntile_all - 1;
@@ -209,8 +272,10 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     const int qw = wave % NQW;
     const int kg = wave / NQW;
     const int q0 = qt * BM;
-    const int hk = h / (a.hq / a.hkv);
-    const int bkv = b / (a.b / a.bk);
+    // (uniform; computed on the vector unit, so moved to scalar registers
+    // for the K/V row addresses, which the LDS copies take as scalars)
+    const int hk = __builtin_amdgcn_readfirstlane(h / (a.hq / a.hkv));
+    const int bkv = __builtin_amdgcn_readfirstlane(b / (a.b / a.bk));
     const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
 
@@ -223,30 +288,55 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // ---- Q operand (B of S^T = K Q^T): row qrow, dims 16ks + 8hh .. +7 ----
     // (the Q element type is a template parameter: a load-or-convert branch on
     // it makes the compiler wait for all global loads inside the KV loop).
-    // Rows past n_q load row 0 and are zeroed, so all loads issue back to back
-    // (before the mask scan, whose loads then share their round trip).
+    // Rows past n_q load row 0 and are zeroed. All loads issue back to back
+    // (with a mask tensor, right after the mask scan's first loads); F32 rows
+    // are held raw and rounded (and rotated) only after the first KV step's
+    // loads are issued, so the first step's loads do not wait for Q. (A branch
+    // on the rotation between one row chunk's loads and the next would make
+    // the compiler wait for each chunk in turn.)
     half8 qb[KS];
-    {
-        constexpr int qelt = QF16 ? 2 : 4;
+    floatx4 qraw[QF16 ? 1 : KS][2];
+    int qpos = 0;   // rotary position of row qrow
+    auto issue_q = [&]() {
         const int64_t qoff = (int64_t)(qvalid ? qrow : 0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            half8 v;
-            if (!QF16 && a.rope_pos) {
-                // rotary embedding of the query row (position of row qrow of batch b)
-                const floatx4* p = (const floatx4*)((const char*)a.q + qoff + (int64_t)(16 * ks + 8 * hh) * 4);
-                const floatx4 x0 = p[0], x1 = p[1];
-                float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                rope8(x, a.rope_pos[(int64_t)b * a.nq + (qvalid ? qrow : 0)], 16 * ks + 8 * hh, a.rope_ts,
-                      a.rope_dims);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = (_Float16)x[e];
+            if constexpr (QF16) {
+                qb[ks] = *(const half8*)((const char*)a.q + qoff + (int64_t)(16 * ks + 8 * hh) * 2);
             } else {
-                v = load_q8(a.q, qoff + (int64_t)(16 * ks + 8 * hh) * qelt, QF16);
+                const floatx4* p = (const floatx4*)((const char*)a.q + qoff + (int64_t)(16 * ks + 8 * hh) * 4);
+                qraw[ks][0] = p[0];
+                qraw[ks][1] = p[1];
             }
-            qb[ks] = qvalid ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
-    }
+        if constexpr (!QF16) {
+            // issued with the Q loads and without a branch (one would make the
+            // compiler wait for every load before it); without a rotary
+            // embedding it reads the first word of Q, unused
+            const int* pp = a.rope_pos ? a.rope_pos + ((int64_t)b * a.nq + (qvalid ? qrow : 0)) : (const int*)a.q;
+            qpos = *pp;
+        }
+    };
+    // With a mask tensor the scan's loads go first and Q's follow them at
+    // once, so the scan waits for its own loads only.
+    if constexpr (MM != 1) issue_q();
+    // rounds the F32 rows to f16 (ggml's Q conversion), rotating them first
+    // when a rotary embedding is given; zeroes rows past n_q
+    auto finish_q = [&]() {
+        if constexpr (!QF16) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                float x[8] = {qraw[ks][0][0], qraw[ks][0][1], qraw[ks][0][2], qraw[ks][0][3],
+                              qraw[ks][1][0], qraw[ks][1][1], qraw[ks][1][2], qraw[ks][1][3]};
+                if (a.rope_pos) rope8(x, qpos, 16 * ks + 8 * hh, a.rope_ts, a.rope_dims);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qb[ks][e] = (_Float16)x[e];
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            if (!qvalid) qb[ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    };
 
     // ---- live column range and tile classes of the mask over this workgroup's
     // rows ----------------------------------------------------------------------
@@ -262,7 +352,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         int lo = 0, hi = 0;
         const int rows = min(BM, a.nq - q0);
         mask_scan_tiles<NT, NQW>((const uint16_t*)((const char*)mplane + (int64_t)q0 * a.m_nb1), a.m_nb1, rows,
-                                 a.nkv, s_tflag, s_red, lo, hi);
+                                 a.nkv, s_tflag, s_red, lo, hi, issue_q);
         step_lo = lo / BS;
         step_hi = hi > lo ? (hi - 1) / BS + 1 : 0;
     } else if constexpr (IMPL) {
@@ -316,7 +406,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     }
     const uint32_t lds_k = lds_offset(sK), lds_v = lds_offset(sV);
     auto issue_step = [&](int s, int stg) {
-        const int kv0 = s * BS;
+        const int kv0 = __builtin_amdgcn_readfirstlane(s) * BS;   // s is uniform
         const uint32_t k_dst = lds_k + stg * TILE_BYTES, v_dst = lds_v + stg * TILE_BYTES;
         if (kv0 + BS <= a.nkv) {
             const char* kst = kb + (int64_t)kv0 * a.k_nb1;
@@ -593,6 +683,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         const int kv0 = s_cur * BS + PF_BN * kg;
         if (MASK && kv0 < a.nkv && tclass(kv0) == 3) load_mask(kv0, mwa);
     }
+    finish_q();
     wait_all_mem();
     __syncthreads();
     while (s_cur >= 0) {
