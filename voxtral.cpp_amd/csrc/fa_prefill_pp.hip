@@ -31,11 +31,16 @@
 //     H2: MFMA  O_B += V_t^T P_B(t)^T, S_B(t+1) = K_{t+1} Q_B^T
 //         VALU  softmax of S_A(t+1) -> P_A(t+1)
 //   The MFMAs of a half do not depend on that half's VALU work, so the
-//   scheduler interleaves them. K_{t+1} and V_t are read at the top of
-//   iteration t; the softmax of S_B(t) needs neither, so the VALU (the
-//   busier pipe for hd 64) can start while the reads land.
+//   scheduler interleaves them. K_{t+1} is read at the top of iteration t
+//   (its block becomes visible at the barrier before); the softmax of S_B(t)
+//   does not need it, so the VALU (the busier pipe for hd 64) can start
+//   while the reads land. V_{t+1} is read in H2 of iteration t, once PV_B(t)
+//   has taken V_t's registers as operands: its block has been visible since
+//   the barrier before iteration t, and the transposed reads (half the LDS
+//   read rate of 128-bit ones) land under H2's work instead of after the
+//   next barrier.
 // K/V staging: an NS-slot LDS ring; block b sits in slot b % NS, its K is
-//   read at the top of iteration b - 1 and its V at the top of iteration b;
+//   read at the top of iteration b - 1 and its V in iteration b - 1 as well;
 //   block b + NS - 1 goes into the slot of block b - 1 at the start of
 //   iteration b, one barrier after that block's last read
 //   (global_load_lds_dwordx4, no staging registers). A block therefore has
@@ -364,8 +369,8 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     // every P of later blocks stays below 2^TAU unless a new larger score
     // arrives, which the same test catches.
     // The basic block of each half (closed by that branch) holds its 8 MFMAs
-    // and the softmax's fast path; HALF (1 or 2) lays them out: in H1 the 12
-    // operand reads first, then softmax VALU work while they land, then one
+    // and the softmax's fast path; HALF (1 or 2) lays them out: in H1 the 4
+    // K operand reads first, then softmax VALU work while they land, then one
     // MFMA per 5 VALU instructions; in H2 (operands in registers) one MFMA per
     // 6 from the start.
     auto softmax_spec = [&](auto half_tag, const floatx16& sc, float& m, float& l, floatx16 (&o)[DB],
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
         constexpr int HALF = decltype(half_tag)::value;
         float ls = exps(sc, m, p);
         if constexpr (HALF == 1) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);   // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS reads
             __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);   // VALU
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -424,6 +429,7 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     }
     if (nf > 0) {
         read_k(0, kr);
+        read_v(0, vr);
         s_mfma(sa, qa, kr);
         s_mfma(sb, qb, kr);
         softmax_exact(sa, ma, la, oa, pa);
@@ -440,7 +446,6 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     for (int t = 0; t + 1 < nf; ++t) {
         if (t + AHEAD < ng) issue(t + AHEAD);
         read_k(t + 1, kr);
-        read_v(t, vr);
         // H1: S_A(t+1), PV_A(t) on the matrix pipe; softmax of S_B(t). The
         // MFMAs come first in the source so they share a basic block with
         // the softmax's fast path (its rare rescale branch closes the block)
@@ -450,6 +455,7 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
         softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb);
         // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
         pv_mfma(ob, pb, vr);
+        read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
         s_mfma(sb, qb, kr);
         softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa);
         // loads of blocks t + 3 .. min(t + 7, ng - 1) may stay in flight
@@ -459,7 +465,6 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     // (no loads are issued from here on)
     if (nf > 0) {
         // last full block: PV_A, softmax of S_B, PV_B
-        read_v(nf - 1, vr);
         pv_mfma(oa, pa, vr);
         softmax_exact(sb, mb, lb, ob, pb);
         pv_mfma(ob, pb, vr);
