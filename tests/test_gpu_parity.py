@@ -158,6 +158,41 @@ def test_prefill_no_mask_gqa(runner):
     check_case(runner, cases.prefill_case(300, causal=False, seed=23))
 
 
+def _sparse_mask(rng, nq, nkv):
+    """-inf everywhere but a few live entries per row, many on the first and
+    last entries of 8-entry groups (where a row's 16-byte chunks straddle
+    64-entry tiles), a fully zero 32 x 64 block, and rows with no live entry."""
+    m = np.full((nq, nkv), cases.NEG_INF_F16, dtype=np.uint16)
+    live_vals = cases.f16_bits(np.array([0.0, 0.0, -1.5, 0.25], dtype=np.float32))
+    for i in range(nq):
+        if i % 11 == 5:
+            continue                      # row without a live entry: output 0
+        cols = set(rng.integers(0, nkv, size=int(rng.integers(1, 4))).tolist())
+        for t in range(0, nkv, 64):       # tile edges and 8-entry group edges
+            for c in (t, t + 7, t + 8, t + 63):
+                if c < nkv and rng.random() < 0.15:
+                    cols.add(c)
+        cols.add(nkv - 1) if rng.random() < 0.3 else None
+        for c in cols:
+            m[i, c] = live_vals[int(rng.integers(0, len(live_vals)))]
+    r1, c1 = min(32, nq), min(64, nkv)
+    m[:r1, :c1] = 0                       # a tile whose entries are all zero
+    return m
+
+
+@pytest.mark.parametrize("n,nkv,hq,hkv,hd", [(71, 133, 32, 8, 128), (129, 511, 32, 8, 128), (64, 65, 32, 8, 128),
+                                           (100, 257, 20, 20, 64), (33, 1001, 16, 8, 128)])
+def test_prefill_sparse_mask_scan(runner, n, nkv, hq, hkv, hd):
+    """The prefill mask scan's tile classes and live range on unpadded rows of
+    odd length (every row misaligned differently), isolated live entries at
+    chunk and tile edges, a partial last tile and a partial last row block;
+    compared with the oracle on the same mask."""
+    rng = np.random.default_rng(1000 + n + nkv)
+    c = cases.prefill_case(n, hq=hq, hkv=hkv, hd=hd, causal=False, kv_offset=nkv - n, seed=900 + n,
+                           name=f"sparse_mask_n{n}_kv{nkv}_hd{hd}")
+    check_case(runner, cases.with_mask(c, _sparse_mask(rng, n, nkv)))
+
+
 @pytest.mark.parametrize("seq", [1, 31, 100, 750, 1501])
 def test_encoder_shapes(runner, seq):
     check_case(runner, cases.encoder_case(seq, 4, 64, seed=300 + seq))
