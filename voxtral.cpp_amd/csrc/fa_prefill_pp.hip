@@ -88,9 +88,8 @@ struct Shape {
     static constexpr int RING = NS * SLOT;
     static constexpr int QST = BM * ROW;        // Q staging: BM rows of 64 f16
     static constexpr int NLD = 4 / NQT;         // K (and V) load instructions per wavefront per block
-    static constexpr int PUB = 2 * 32 + 4;      // floats a merging wavefront publishes per lane
-    static constexpr int XS = (KVG - 1) * NQT * PUB * 64 * 4;   // merge area
-    static constexpr int OST = (XS + 255) / 256 * 256;        // output staging tile
+    static constexpr int PUB = 2 * 32 + 4;      // floats each wavefront publishes per lane for the merge
+    static constexpr int XS = KVG * NQT * PUB * 64 * 4;       // merge area (then the output staging tile)
 };
 // one wavefront per SIMD (4 wavefronts, 8-slot ring)
 using Shape1 = Shape<2, 2, 8>;
@@ -131,7 +130,7 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     constexpr int AHEAD = SH::AHEAD, SLOT = SH::SLOT, RING = SH::RING, QST = SH::QST, NLD = SH::NLD;
     static_assert(NLD * NQT == 4, "a block's 4 load instructions per matrix split evenly");
     static_assert(8 * 2 * NLD < 64 && NS <= 8, "vmcnt range of wait_blocks");
-    static_assert(SH::OST + BM * 256 <= RING + QST, "merge and output staging fit the LDS");
+    static_assert(SH::XS <= RING + QST && BM * 256 <= RING + QST, "merge and output staging fit the LDS");
     __shared__ __attribute__((aligned(16))) char smem[RING + QST];
 
     // ---- XCD-aware position of this workgroup --------------------------------
@@ -489,15 +488,20 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     for (int tt = ng; tt < ni; ++tt) __syncthreads();
 
     // ---- merge the KV groups through LDS (the ring is free), normalise ------------
-    // Groups 1.. publish (O, m, l) element-major (each wavefront's 64 lanes
-    // write consecutive words); group 0 merges and writes the normalised rows
-    // to a staging tile, row r at r * 256 bytes with 16-byte chunk j at
-    // position j ^ (r & 15); then all wavefronts store full rows.
+    // Every wavefront publishes its (O, m, l) element-major (its 64 lanes write
+    // consecutive words). Wavefront (kg, wq) then merges 64 / KVG of the 64
+    // O elements of query tile wq over all groups (all of one half, A or B),
+    // in group order, and after a barrier (the staging tile overlaps the
+    // published data) writes them normalised to the staging tile, row r at
+    // r * 256 bytes with 16-byte chunk j at position j ^ (r & 15); then all
+    // wavefronts store full rows.
     constexpr int PUB = SH::PUB;
+    constexpr int EPW = 64 / KVG;                   // elements merged per wavefront
+    static_assert(EPW % 4 == 0 && EPW <= 32, "a wavefront's elements lie in one half");
     float* xs = (float*)smem;
-    char* ost = smem + SH::OST;
-    if (kg > 0) {
-        float* w = xs + ((kg - 1) * NQT + wq) * PUB * 64 + lane;
+    char* ost = smem;
+    {
+        float* w = xs + (kg * NQT + wq) * PUB * 64 + lane;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -511,47 +515,50 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
         w[67 * 64] = lb;
     }
     __syncthreads();
-    if (kg == 0) {
+    const int e0 = kg * EPW;        // first element: 0..31 half A, 32..63 half B
+    const int x = e0 / 32;
+    floatx4 res[EPW / 4];
+    {
+        float mg[KVG], lg[KVG];
+        float M = -INFINITY;
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            const float m = x ? mb : ma;
-            const float l = x ? lb : la;
-            const floatx16 (&o)[DB] = x ? ob : oa;
-            float M = m;
+        for (int g = 0; g < KVG; ++g) {
+            const float* r = xs + (g * NQT + wq) * PUB * 64 + lane;
+            mg[g] = r[(64 + x) * 64];
+            lg[g] = r[(66 + x) * 64];
+            M = fmaxf(M, mg[g]);
+        }
+        const float Ms = (M == -INFINITY) ? 0.f : M;
+        float wg[KVG];
+        float lsum = 0.f;
 #pragma unroll
-            for (int g = 1; g < KVG; ++g) M = fmaxf(M, xs[((g - 1) * NQT + wq) * PUB * 64 + (64 + x) * 64 + lane]);
-            const float Ms = (M == -INFINITY) ? 0.f : M;
-            const float w0 = exp2_fast(m - Ms);
-            float wg[KVG > 1 ? KVG - 1 : 1];
-            float lsum = l * w0;
+        for (int g = 0; g < KVG; ++g) {
+            wg[g] = exp2_fast(mg[g] - Ms);
+            lsum = fmaf(wg[g], lg[g], lsum);
+        }
+        const float lt = pair32_sum(lsum);
+        const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
 #pragma unroll
-            for (int g = 1; g < KVG; ++g) {
-                const float* r = xs + ((g - 1) * NQT + wq) * PUB * 64 + lane;
-                wg[g - 1] = exp2_fast(r[(64 + x) * 64] - Ms);
-                lsum = fmaf(wg[g - 1], r[(66 + x) * 64], lsum);
+        for (int g = 0; g < KVG; ++g) wg[g] *= inv;
+#pragma unroll
+        for (int q = 0; q < EPW / 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float acc = 0.f;
+#pragma unroll
+                for (int g = 0; g < KVG; ++g)
+                    acc = fmaf(wg[g], xs[(g * NQT + wq) * PUB * 64 + (e0 + 4 * q + e) * 64 + lane], acc);
+                res[q][e] = acc;
             }
-            const float lt = pair32_sum(lsum);
-            const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
-            const float f0 = w0 * inv;
+    }
+    __syncthreads();   // every read of the published data is done
+    {
+        const int row = 64 * wq + 32 * x + nl;
 #pragma unroll
-            for (int g = 1; g < KVG; ++g) wg[g - 1] *= inv;
-            const int row = 64 * wq + 32 * x + nl;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    floatx4 v;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float acc = o[db][4 * a4 + e] * f0;
-#pragma unroll
-                        for (int g = 1; g < KVG; ++g)
-                            acc = fmaf(wg[g - 1], xs[((g - 1) * NQT + wq) * PUB * 64 + (32 * x + db * 16 + 4 * a4 + e) * 64 + lane], acc);
-                        v[e] = acc;
-                    }
-                    const int ch = 8 * db + 2 * a4 + hh;   // dims 4 ch .. 4 ch + 3
-                    *(floatx4*)(ost + row * 256 + ((ch ^ (row & 15)) * 16)) = v;
-                }
+        for (int q = 0; q < EPW / 4; ++q) {
+            const int eh = e0 - 32 * x + 4 * q;              // element within the half: 16 db + 4 a4
+            const int ch = 8 * (eh / 16) + 2 * ((eh % 16) / 4) + hh;   // dims 4 ch .. 4 ch + 3
+            *(floatx4*)(ost + row * 256 + ((ch ^ (row & 15)) * 16)) = res[q];
         }
     }
     __syncthreads();
