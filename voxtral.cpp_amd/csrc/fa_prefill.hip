@@ -146,8 +146,8 @@ __device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t ro
         for (int j = 0; j < 4; ++j) hmi[bt][j] = half_mask(m8i[bt], j);
     }
     int tlo = 0x7fffffff, thi = -1;                // live tiles (wave-uniform)
-    // The first batch is straight-line code: at a loop's head the compiler
-    // would wait for the loads issued before the scan (Q) first.
+    // The first batch is straight-line code, so no wait a loop's head would
+    // get for loads issued earlier comes before its loads and Q's.
     auto batch = [&](int ub, bool first) {
         u32x4 w[UB][5];
         bool okr[UB][5];
