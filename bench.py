@@ -100,25 +100,27 @@ def encoder_layers(torch, n_layers, seq=1500, heads=20, hd=64, seed=1000):
 
 
 def decode_layers(torch, n_layers, n_kv, hq=32, hkv=8, hd=128, capacity=None, seed=2000, batch=1,
-                  kv_sigma=1.0, masks=None):
+                  kv_sigma=1.0, masks=None, kv_f32=False):
     cap = capacity or n_kv
+    kvt = torch.float32 if kv_f32 else torch.float16
     out = []
     for i in range(n_layers):
         q = randn(torch, (batch, 1, hq, hd), seed + 3 * i)
-        k = randn(torch, (batch, cap, hkv, hd), seed + 3 * i + 1, kv_sigma, torch.float16)
-        v = randn(torch, (batch, cap, hkv, hd), seed + 3 * i + 2, kv_sigma, torch.float16)
+        k = randn(torch, (batch, cap, hkv, hd), seed + 3 * i + 1, kv_sigma, kvt)
+        v = randn(torch, (batch, cap, hkv, hd), seed + 3 * i + 2, kv_sigma, kvt)
         dst = torch.empty(batch * hq * hd, device="cuda", dtype=torch.float32)
         qne, qnb = views.decoder_q(1, hq, hd)
         qne = (qne[0], qne[1], qne[2], batch)
         qnb = (qnb[0], qnb[1], qnb[2], hq * hd * 4)
-        kne, knb = views.kv_cache(n_kv, hkv, hd, cap, batch=batch)
+        kne, knb = views.kv_cache(n_kv, hkv, hd, cap, elt=4 if kv_f32 else 2, batch=batch)
+        kty = vxfa.F32 if kv_f32 else vxfa.F16
         md = None
         if masks is not None:
             m = masks
             md = vxfa.desc(m.data_ptr(), vxfa.F16, *views.mask(n_kv, 1, 1, batch))
         out.append(Layer(vxfa.desc(q.data_ptr(), vxfa.F32, qne, qnb),
-                         vxfa.desc(k.data_ptr(), vxfa.F16, kne, knb),
-                         vxfa.desc(v.data_ptr(), vxfa.F16, kne, knb),
+                         vxfa.desc(k.data_ptr(), kty, kne, knb),
+                         vxfa.desc(v.data_ptr(), kty, kne, knb),
                          md,
                          vxfa.desc(dst.data_ptr(), vxfa.F32, *views.dst(hd, hq, 1, batch)),
                          f32s(1.0 / math.sqrt(hd)), (q, k, v, dst, masks)))
@@ -205,8 +207,8 @@ def time_calls(torch, ctx, calls, steps, warmup, graph=True):
     return ms / steps, 1000.0 * ms / (steps * len(calls))
 
 
-def decode_bytes(n_live, hq=32, hkv=8, hd=128, mask_bytes=0):
-    return n_live * hkv * hd * 2 * 2 + hq * hd * 4 * 2 + mask_bytes
+def decode_bytes(n_live, hq=32, hkv=8, hd=128, mask_bytes=0, elt=2):
+    return n_live * hkv * hd * elt * 2 + hq * hd * 4 * 2 + mask_bytes
 
 
 # ---------------------------------------------------------------------------
@@ -329,14 +331,18 @@ def main():
     torch.cuda.empty_cache()
 
     if want("decode"):
-        for n_kv, layers in ((1024, 30), (8192, 30)):
+        # cold: enough distinct layer caches that one step's reads exceed the
+        # 256 MB MALL (n_kv 1024: 80 x 4.2 MB; n_kv 8192: 30 x 33.6 MB)
+        for n_kv, layers in ((1024, 80), (8192, 30)):
             dl = decode_layers(torch, layers, n_kv, seed=2000 + n_kv)
             _, us = time_calls(torch, ctx, dl, K, W)
             by = decode_bytes(n_kv)
             gbs = by / (us * 1e-6) / 1e9
             log(f"[decode n_kv={n_kv}] {us:.2f} us/layer  {gbs:.0f} GB/s")
             configs[f"decode_nkv{n_kv}"] = {"us_per_layer": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
-                                            "bytes_per_layer": by, "layers": layers, "cache": "cold (30 layers)"}
+                                            "bytes_per_layer": by, "layers": layers,
+                                            "cache": f"cold ({layers} layer caches, {layers * by / 1e6:.0f} MB "
+                                                     "per step > 256 MB MALL)"}
             if n_kv == 8192:
                 # the new token's K/V (F32, one 1024-float row each) appended to the f16 cache:
                 # fused into the attention launch, and as a separate append launch
@@ -364,6 +370,16 @@ def main():
                 del news
             del dl
             torch.cuda.empty_cache()
+        # the reference's own F32 cache (src/voxtral.cpp:1126-1136), read in place
+        dl = decode_layers(torch, 30, 8192, seed=2500, kv_f32=True)
+        _, us = time_calls(torch, ctx, dl, K, W)
+        by = decode_bytes(8192, elt=4)
+        gbs = by / (us * 1e-6) / 1e9
+        log(f"[decode n_kv=8192, F32 cache] {us:.2f} us/layer  {gbs:.0f} GB/s")
+        configs["decode_nkv8192_f32_cache"] = {"us_per_layer": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                                               "bytes_per_layer": by, "layers": 30, "cache": "cold (30 layers)"}
+        del dl
+        torch.cuda.empty_cache()
 
     if want("prefill"):
         pl = prefill_layers(torch, 30)

@@ -17,8 +17,8 @@
  *
  * Tensor contract (ggml order, ne[0] fastest, nb in bytes):
  *   q    [D,  Nq,  Hq,  B ]  F32 or F16, rows contiguous (nb[0] = elt size)
- *   k    [D,  Nkv, Hkv, Bk]  F16, rows contiguous
- *   v    [D,  Nkv, Hkv, Bk]  F16, rows contiguous (not transposed)
+ *   k    [D,  Nkv, Hkv, Bk]  F16 or F32, rows contiguous
+ *   v    [D,  Nkv, Hkv, Bk]  same type as k, rows contiguous (not transposed)
  *   mask [Nkv, >=Nq, Hm, Bm] F16 additive (0 / -inf in voxtral), nullable,
  *                            elements contiguous along ne[0]
  *   dst  [D,  Hq,  Nq,  B ]  F32, contiguous (permuted relative to q)
@@ -57,7 +57,7 @@ enum vxfa_status {
     VXFA_OK           = 0,
     VXFA_UNSUPPORTED  = 1,  /* valid op, but this path does not implement it  */
     VXFA_INVALID_ARG  = 2,  /* violates the ggml contract (shapes, strides)   */
-    VXFA_NO_WORKSPACE = 3,  /* could not allocate the split-KV workspace      */
+    VXFA_NO_WORKSPACE = 3,  /* the context's fixed workspace is too small     */
     VXFA_HIP_ERROR    = 4,  /* a HIP call failed; see vxfa_last_error()       */
 };
 
@@ -71,13 +71,22 @@ typedef struct vxfa_tensor {
     size_t  nb[4];
 } vxfa_tensor;
 
-/* Per-stream context. Owns the split-KV workspace (partial O, running max
- * and sum per split, plus arrival counters) and grows it on demand; the
+/* Per-stream context (the analogue of a ggml backend context). Owns one
+ * device workspace of fixed size, allocated by vxfa_ctx_create and freed by
+ * vxfa_ctx_destroy: the split-KV arrival counters, the split-KV partial
+ * records (partial O, running max and sum per split) and an f16 staging
+ * area for F32 K/V of prefill calls (32 MiB: K and V of up to 8192 rows of
+ * 8 x 128). No other call allocates, frees or synchronises, so every call
+ * can be captured into a HIP graph; a decode call whose batch would need more
+ * partial records than the workspace holds runs with fewer splits, a prefill
+ * call with F32 K/V beyond the staging area returns VXFA_NO_WORKSPACE. The
  * caller's tensors are never allocated or freed here. One context per
  * stream; calls on one context must not overlap. */
 typedef struct vxfa_ctx vxfa_ctx;
 
-/* Create a context bound to HIP device `device`. Returns NULL on failure. */
+/* Create a context bound to HIP device `device` and allocate its workspace
+ * (about 50 MiB; the counters are zeroed and the device synchronised before
+ * it returns). Returns NULL on failure. */
 vxfa_ctx* vxfa_ctx_create(int device);
 
 /* Destroy a context and free its workspace. NULL is accepted. */
@@ -97,8 +106,12 @@ int vxfa_supports(const vxfa_tensor* q, const vxfa_tensor* k,
 /* Execute GGML_OP_FLASH_ATTN_EXT. Replaces the backend kernel behind
  * ggml_flash_attn_ext(ctx, q, k, v, mask, scale, max_bias, logit_softcap)
  * at src/voxtral.cpp:1611 and :1802. Asynchronous on `stream`: the call
- * returns after the launches are queued. Output is deterministic for equal
- * inputs (fixed split boundaries and combine order). */
+ * returns after the launches are queued, with no host synchronisation and no
+ * allocation. Output is deterministic for equal inputs (fixed split
+ * boundaries and merge order). F32 K/V (the reference's own cache,
+ * src/voxtral.cpp:1126-1136, and the encoder's K/V, :1581-1605) are rounded
+ * to f16 for the QK^T product (as Q is); a decode step reads them in place,
+ * a prefill call copies them to f16 in the context's staging area first. */
 int vxfa_flash_attn_ext(vxfa_ctx* ctx, const vxfa_tensor* q,
                         const vxfa_tensor* k, const vxfa_tensor* v,
                         const vxfa_tensor* mask, vxfa_tensor* dst, float scale,

@@ -13,9 +13,9 @@
  *     Qq   = Q row converted to K's dot type (f16 when K is f16)
  *     M = -inf, S = 0, VKQ = 0 (f16 array when V is f16, else f32)
  *     for each kv position ic:
- *       mv = slope * mask[ic]          (0 when no mask)
+ *       mv = mask[ic]                  (0 when no mask)
  *       if mv == -inf: skip the position
- *       s  = dot(K row, Qq) * scale    (softcap: s = c * tanh(s), scale /= c)
+ *       s  = dot(K row, Qq) * scale
  *       s += mv
  *       if s > M: M = s, ms = exp(Mold - M), VKQ *= ms, vs = 1
  *       else    : ms = 1, vs = exp(s - M)
@@ -27,6 +27,11 @@
  * views over the token-major KV cache, mask cast to F16 at :1801). Mask
  * values come from :2104-2111 (causal) and :2179-2190 (encoder window).
  * Thread count default in the reference: min(hw, 16) at :1046-1051.
+ *
+ * voxtral passes max_bias = 0 and logit_softcap = 0 at both call sites, and
+ * the HIP path reports anything else as unsupported; ggml's ALiBi slope and
+ * tanh soft-capping are therefore not restated here, and both routines
+ * reject nonzero values as a contract violation.
  *
  * The f64 routine is an exact two-pass softmax used to pin the restatement.
  */
@@ -115,15 +120,6 @@ static int check_contract(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa
     return 0;
 }
 
-/* ALiBi slope for head h (ggml's max_bias convention); 1 when max_bias == 0 */
-static float alibi_slope(float max_bias, uint32_t n_head, uint32_t h) {
-    if (!(max_bias > 0.0f)) return 1.0f;
-    const uint32_t n_head_log2 = 1u << (uint32_t)floor(log2((double)n_head));
-    const float m0 = powf(2.0f, -(max_bias) / (float)n_head_log2);
-    const float m1 = powf(2.0f, -(max_bias / 2.0f) / (float)n_head_log2);
-    return h < n_head_log2 ? powf(m0, (float)(h + 1)) : powf(m1, (float)(2 * (h - n_head_log2) + 1));
-}
-
 /* ------------------------------------------------------------------ */
 /* threading helper */
 
@@ -164,7 +160,7 @@ static void parallel_rows(int64_t nrows, int n_threads,
 typedef struct {
     const vxfa_tensor *q, *k, *v, *mask;
     vxfa_tensor* dst;
-    float scale, max_bias, softcap;
+    float scale;
     int flags;
 } ggml_job_t;
 
@@ -211,8 +207,6 @@ static void ggml_rows(void* arg, int64_t ir0, int64_t ir1, int ith) {
     const int flags = J->flags;
 
     float scale = J->scale;
-    const float softcap = J->softcap;
-    if (softcap != 0.0f) scale /= softcap;
     if (flags & ORACLE_MUT_NO_SCALE) scale = 1.0f;
 
     const int k_f16 = k->type == VXFA_TYPE_F16;
@@ -230,7 +224,6 @@ static void ggml_rows(void* arg, int64_t ir0, int64_t ir1, int ith) {
         const int64_t iq2 = (ir - iq3 * Hq * Nq) / Nq;
         const int64_t iq1 = ir - iq3 * Hq * Nq - iq2 * Nq;
 
-        const float slope = alibi_slope(J->max_bias, (uint32_t)Hq, (uint32_t)iq2);
         const int64_t ik2 = (flags & ORACLE_MUT_GQA_MOD) ? iq2 % k->ne[2] : iq2 / rk2;
         const int64_t ik3 = iq3 / rk3;
 
@@ -248,7 +241,7 @@ static void ggml_rows(void* arg, int64_t ir0, int64_t ir1, int ith) {
         else memset(VKQ32, 0, sizeof(float) * DV);
 
         for (int64_t ic = 0; ic < nkv; ++ic) {
-            const float mv = mp ? slope * oracle_f16_to_f32(mp[ic]) : 0.0f;
+            const float mv = mp ? oracle_f16_to_f32(mp[ic]) : 0.0f;
             if (mv == -INFINITY) continue;
 
             const char* krow = (const char*)k->data + ic * k->nb[1] + ik2 * k->nb[2] + ik3 * k->nb[3];
@@ -260,7 +253,6 @@ static void ggml_rows(void* arg, int64_t ir0, int64_t ir1, int ith) {
                 s = dot_f32(Kf, Qf, DK);
             }
             s = s * scale;
-            if (softcap != 0.0f) s = softcap * tanhf(s);
             s += mv;
 
             const float Mold = M;
@@ -308,7 +300,8 @@ int oracle_fa_ggml(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor
                    const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias,
                    float logit_softcap, int flags, int n_threads) {
     if (check_contract(q, k, v, mask, dst, 1)) return -1;
-    ggml_job_t J = {q, k, v, mask, dst, scale, max_bias, logit_softcap, flags};
+    if (max_bias != 0.0f || logit_softcap != 0.0f) return -1;
+    ggml_job_t J = {q, k, v, mask, dst, scale, flags};
     const int64_t nrows = q->ne[1] * q->ne[2] * q->ne[3];
     if (nrows == 0) return 0;
     parallel_rows(nrows, n_threads, ggml_rows, &J);
@@ -321,7 +314,7 @@ int oracle_fa_ggml(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor
 typedef struct {
     const vxfa_tensor *q, *k, *v, *mask;
     double* dst;
-    float scale, max_bias, softcap;
+    float scale;
     int q_f16;
 } f64_job_t;
 
@@ -336,15 +329,13 @@ static void f64_rows(void* arg, int64_t ir0, int64_t ir1, int ith) {
     double* qd = (double*)malloc(sizeof(double) * DK);
     double* sc = (double*)malloc(sizeof(double) * (nkv > 0 ? nkv : 1));
     double* acc = (double*)malloc(sizeof(double) * DV);
-    const double softcap = J->softcap;
-    const double scale = softcap != 0.0 ? (double)J->scale / softcap : (double)J->scale;
+    const double scale = (double)J->scale;
 
     for (int64_t ir = ir0; ir < ir1; ++ir) {
         const int64_t iq3 = ir / (Hq * Nq);
         const int64_t iq2 = (ir - iq3 * Hq * Nq) / Nq;
         const int64_t iq1 = ir - iq3 * Hq * Nq - iq2 * Nq;
         const int64_t ik2 = iq2 / rk2, ik3 = iq3 / rk3;
-        const double slope = alibi_slope(J->max_bias, (uint32_t)Hq, (uint32_t)iq2);
 
         const char* qrow = (const char*)q->data + iq1 * q->nb[1] + iq2 * q->nb[2] + iq3 * q->nb[3];
         for (int64_t d = 0; d < DK; ++d) {
@@ -358,13 +349,12 @@ static void f64_rows(void* arg, int64_t ir0, int64_t ir1, int ith) {
                                    (iq2 % mask->ne[2]) * mask->nb[2] + (iq3 % mask->ne[3]) * mask->nb[3]);
         double M = -INFINITY;
         for (int64_t ic = 0; ic < nkv; ++ic) {
-            const double mv = mp ? slope * (double)oracle_f16_to_f32(mp[ic]) : 0.0;
+            const double mv = mp ? (double)oracle_f16_to_f32(mp[ic]) : 0.0;
             if (mv == -INFINITY) { sc[ic] = -INFINITY; continue; }
             const char* krow = (const char*)k->data + ic * k->nb[1] + ik2 * k->nb[2] + ik3 * k->nb[3];
             double s = 0.0;
             for (int64_t d = 0; d < DK; ++d) s += qd[d] * (double)load_elt(krow + d * k->nb[0], k->type);
             s *= scale;
-            if (softcap != 0.0) s = softcap * tanh(s);
             s += mv;
             sc[ic] = s;
             if (s > M) M = s;
@@ -390,7 +380,8 @@ int oracle_fa_f64(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor*
                   const vxfa_tensor* mask, double* dst, float scale, float max_bias,
                   float logit_softcap, int q_f16, int n_threads) {
     if (!dst || check_contract(q, k, v, mask, NULL, 0)) return -1;
-    f64_job_t J = {q, k, v, mask, dst, scale, max_bias, logit_softcap, q_f16};
+    if (max_bias != 0.0f || logit_softcap != 0.0f) return -1;
+    f64_job_t J = {q, k, v, mask, dst, scale, q_f16};
     const int64_t nrows = q->ne[1] * q->ne[2] * q->ne[3];
     if (nrows == 0) return 0;
     parallel_rows(nrows, n_threads, f64_rows, &J);

@@ -38,7 +38,9 @@ enum {
  * skipped, online softmax with expf, V accumulated in f16 or f32, output
  * scaled by 1/S (0 when S == 0), written in the permuted dst layout.
  * Threads: rows are split across n_threads (<= 0 means 1).
- * Returns 0, or -1 on a contract violation. */
+ * max_bias and logit_softcap must be 0 (voxtral's arguments; ALiBi and
+ * soft-capping are not restated). Returns 0, or -1 on a contract violation
+ * or a nonzero max_bias / logit_softcap. */
 int oracle_fa_ggml(const vxfa_tensor* q, const vxfa_tensor* k,
                    const vxfa_tensor* v, const vxfa_tensor* mask,
                    vxfa_tensor* dst, float scale, float max_bias,
@@ -46,7 +48,8 @@ int oracle_fa_ggml(const vxfa_tensor* q, const vxfa_tensor* k,
 
 /* Exact reference in double precision: two-pass softmax over the unmasked
  * positions. q_f16 != 0 rounds Q to f16 first (as ggml does for f16 K).
- * Fully masked rows give zeros. dst is double [D, Hq, Nq, B] contiguous. */
+ * Fully masked rows give zeros. dst is double [D, Hq, Nq, B] contiguous.
+ * max_bias and logit_softcap must be 0, as above. */
 int oracle_fa_f64(const vxfa_tensor* q, const vxfa_tensor* k,
                   const vxfa_tensor* v, const vxfa_tensor* mask,
                   double* dst, float scale, float max_bias,

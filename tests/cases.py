@@ -70,9 +70,10 @@ class Case:
 
 
 def decode_case(n_kv, hq=32, hkv=8, hd=128, capacity=None, seed=1, q_sigma=1.0, kv_sigma=1.0,
-                batch=1, window=None, name=None, q_f16=False):
+                batch=1, window=None, name=None, q_f16=False, kv_f32=False):
     """Single-token decode against a token-major f16 cache (src/voxtral.cpp:1736-1805).
-    window: if set, additive mask [n_kv, 1] with -inf outside the last `window` rows."""
+    window: if set, additive mask [n_kv, 1] with -inf outside the last `window` rows.
+    kv_f32: the cache is F32, the reference's own cache type (:1126-1136)."""
     rng = np.random.default_rng(seed)
     cap = capacity or n_kv
     c = Case(name or f"decode_nkv{n_kv}_b{batch}", f32(1.0 / math.sqrt(hd)))
@@ -83,14 +84,27 @@ def decode_case(n_kv, hq=32, hkv=8, hd=128, capacity=None, seed=1, q_sigma=1.0, 
         c.add("q", "q", q, F32, *_batched_q(1, hq, hd, 4, batch))
     k = f16_bits(normal(rng, (batch, cap, hkv, hd), kv_sigma))
     v = f16_bits(normal(rng, (batch, cap, hkv, hd), kv_sigma))
-    ne, nb = views.kv_cache(n_kv, hkv, hd, cap, batch=batch)
-    c.add("k", "k", k, F16, ne, nb)
-    c.add("v", "v", v, F16, ne, nb)
+    if kv_f32:
+        k, v = _widen(k), _widen(v)
+    ne, nb = views.kv_cache(n_kv, hkv, hd, cap, elt=4 if kv_f32 else 2, batch=batch)
+    c.add("k", "k", k, F32 if kv_f32 else F16, ne, nb)
+    c.add("v", "v", v, F32 if kv_f32 else F16, ne, nb)
     if window is not None:
         m = np.zeros((batch, 1, n_kv), dtype=np.uint16)
         m[:, :, : max(0, n_kv - window)] = NEG_INF_F16
         c.add("mask", "mask", m, F16, *views.mask(n_kv, 1, 1, batch))
     return c
+
+
+def _widen(h, perturb=True):
+    """f16 bits -> F32 values. With perturb, each value moves by a few f16 ulps
+    of pseudo-random F32 detail, so F32 inputs are not f16-valued (the path
+    must round them itself, as it rounds Q)."""
+    x = h.view(np.float16).astype(np.float32)
+    if perturb:
+        r = np.random.default_rng(x.size).uniform(-1.0, 1.0, size=x.shape).astype(np.float32)
+        x = (x + r * np.abs(x) * np.float32(2.0 ** -9)).astype(np.float32)
+    return np.ascontiguousarray(x)
 
 
 def _batched_q(n_tokens, heads, hd, elt, batch):
@@ -99,13 +113,14 @@ def _batched_q(n_tokens, heads, hd, elt, batch):
 
 
 def encoder_case(seq=1500, heads=20, hd=64, seed=2, name=None, window=None, scale=None, q_f16=False,
-                 k_ramp=0.0, q_sigma=1.0):
+                 k_ramp=0.0, q_sigma=1.0, kv_f32=False):
     """Encoder self-attention (src/voxtral.cpp:1580-1613): q/k/v [hd, seq, heads]
     views of [seq][heads][hd] buffers. q is f16-valued, stored as F32 (the
     reference's q is a mul_mat output) or, with q_f16, as F16; window: realtime
     sliding-causal mask (src/voxtral.cpp:2179-2190). k_ramp > 0 scales key row
     j by 1 + k_ramp * j / seq, so row maxima keep growing along the KV axis.
-    scale defaults to 1/sqrt(hd)."""
+    scale defaults to 1/sqrt(hd). kv_f32: K/V are F32, as the reference's
+    mul_mat outputs are (src/voxtral.cpp:1581-1605)."""
     rng = np.random.default_rng(seed)
     c = Case(name or f"encoder_seq{seq}", f32(1.0 / math.sqrt(hd) if scale is None else scale))
     qh = f16_bits(normal(rng, (seq, heads, hd), q_sigma))
@@ -119,8 +134,12 @@ def encoder_case(seq=1500, heads=20, hd=64, seed=2, name=None, window=None, scal
         c.add("q", "q", qh, F16, *views.encoder_qkv(seq, heads, hd, 2))
     else:
         c.add("q", "q", q, F32, *views.encoder_qkv(seq, heads, hd, 4))
-    c.add("k", "k", k, F16, *views.encoder_qkv(seq, heads, hd, 2))
-    c.add("v", "v", v, F16, *views.encoder_qkv(seq, heads, hd, 2))
+    if kv_f32:
+        c.add("k", "k", _widen(k), F32, *views.encoder_qkv(seq, heads, hd, 4))
+        c.add("v", "v", _widen(v), F32, *views.encoder_qkv(seq, heads, hd, 4))
+    else:
+        c.add("k", "k", k, F16, *views.encoder_qkv(seq, heads, hd, 2))
+        c.add("v", "v", v, F16, *views.encoder_qkv(seq, heads, hd, 2))
     if window is not None:
         qi = np.arange(seq)[:, None]
         ki = np.arange(seq)[None, :]
@@ -130,9 +149,11 @@ def encoder_case(seq=1500, heads=20, hd=64, seed=2, name=None, window=None, scal
     return c
 
 
-def prefill_case(n=439, hq=32, hkv=8, hd=128, seed=3, causal=True, kv_offset=0, capacity=None, name=None):
+def prefill_case(n=439, hq=32, hkv=8, hd=128, seed=3, causal=True, kv_offset=0, capacity=None, name=None,
+                 kv_f32=False):
     """Decoder prefill (src/voxtral.cpp:1736-1805) with the causal mask of
-    fill_causal_mask (:2104-2111); kv_offset > 0 gives n_kv = kv_offset + n."""
+    fill_causal_mask (:2104-2111); kv_offset > 0 gives n_kv = kv_offset + n.
+    kv_f32: the reference's F32 cache (:1126-1136)."""
     rng = np.random.default_rng(seed)
     n_kv = kv_offset + n
     cap = capacity or n_kv
@@ -141,9 +162,11 @@ def prefill_case(n=439, hq=32, hkv=8, hd=128, seed=3, causal=True, kv_offset=0, 
     c.add("q", "q", q, F32, *views.decoder_q(n, hq, hd))
     k = f16_bits(normal(rng, (cap, hkv, hd)))
     v = f16_bits(normal(rng, (cap, hkv, hd)))
-    ne, nb = views.kv_cache(n_kv, hkv, hd, cap)
-    c.add("k", "k", k, F16, ne, nb)
-    c.add("v", "v", v, F16, ne, nb)
+    if kv_f32:
+        k, v = _widen(k), _widen(v)
+    ne, nb = views.kv_cache(n_kv, hkv, hd, cap, elt=4 if kv_f32 else 2)
+    c.add("k", "k", k, F32 if kv_f32 else F16, ne, nb)
+    c.add("v", "v", v, F32 if kv_f32 else F16, ne, nb)
     if causal:
         qi = np.arange(n)[:, None] + kv_offset
         ki = np.arange(n_kv)[None, :]
@@ -229,13 +252,13 @@ def rope_ggml(x, positions, n_dims, freq_base):
 
 
 def batched_case(n_streams=32, hq=32, hkv=8, hd=128, capacity=8192, lo=512, hi=8192, seed=5,
-                 kv_sigma=0.5, name=None):
+                 kv_sigma=0.5, name=None, kv_f32=False):
     """32 independent decode streams along ne[3] with ragged valid lengths
     drawn from U{lo..hi} and a per-stream length mask [cap, 1, 1, B]."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(lo, hi + 1, size=n_streams)
     c = decode_case(capacity, hq, hkv, hd, capacity=capacity, seed=seed + 1000, kv_sigma=kv_sigma,
-                    batch=n_streams, name=name or f"batched_{n_streams}")
+                    batch=n_streams, name=name or f"batched_{n_streams}", kv_f32=kv_f32)
     m = np.zeros((n_streams, 1, capacity), dtype=np.uint16)
     for b, L in enumerate(lens):
         m[b, 0, L:] = NEG_INF_F16
@@ -252,7 +275,14 @@ def oracle_ggml(c: Case, vkq_f16=False, flags=0, threads=None):
                           c.scale, vkq_f16=vkq_f16, flags=flags, threads=threads)
 
 
-def oracle_f64(c: Case, threads=None):
+def q_rounded(c: Case) -> bool:
+    """ggml converts Q to K's dot type: f16 for an f16 K, none for an F32 K."""
+    return c.views["k"][1] == F16
+
+
+def oracle_f64(c: Case, threads=None, q_f16=None):
+    """Exact float64 attention; Q rounded to f16 when K is f16 (ggml's Q
+    conversion), unless q_f16 says otherwise."""
     from oracle import oracle
     return oracle.fa_f64(c.oracle_view("q"), c.oracle_view("k"), c.oracle_view("v"), c.oracle_view("mask"),
-                         c.scale, threads=threads)
+                         c.scale, q_f16=q_rounded(c) if q_f16 is None else q_f16, threads=threads)

@@ -39,10 +39,14 @@ def expand(case):
     return q, k, v, m
 
 
-def sdpa_f64(case, q_f16=True):
-    """torch SDPA in float64; returns [B, Nq, Hq, D] and a mask of live rows."""
+def sdpa_f64(case, q_f16=None):
+    """torch SDPA in float64; returns [B, Nq, Hq, D] and a mask of live rows.
+    Q is rounded to f16 first when q_f16, by default when K is f16 (ggml
+    converts Q to K's dot type)."""
     import torch
 
+    if q_f16 is None:
+        q_f16 = case.views["k"][1] == F16
     q, k, v, m = expand(case)
     if q_f16:
         q = q.astype(np.float16).astype(np.float64)

@@ -75,6 +75,10 @@ def supports(c, **over):
     lambda: cases.encoder_case(64, 20, 64, seed=1),
     lambda: cases.prefill_case(40, seed=1),
     lambda: cases.batched_case(4, capacity=64, lo=2, hi=64, seed=1),
+    # the reference's own F32 cache and F32 encoder K/V (src/voxtral.cpp:1126-1136, :1581-1605)
+    lambda: cases.decode_case(1024, seed=1, kv_f32=True),
+    lambda: cases.encoder_case(64, 20, 64, seed=1, kv_f32=True),
+    lambda: cases.prefill_case(40, seed=1, kv_f32=True),
 ])
 def test_voxtral_views_are_supported(make):
     assert supports(make()) == vxfa.OK
@@ -85,8 +89,11 @@ def test_unsupported_features_report_unsupported():
     assert supports(c, max_bias=8.0) == vxfa.UNSUPPORTED
     assert supports(c, softcap=30.0) == vxfa.UNSUPPORTED
     d = descs(c)
+    # F32 K with f16 V: mixed K/V types are not implemented
     k32 = vxfa.desc(ADDR, vxfa.F32, d["k"].ne, [4, 4096, 512, 4096 * 64])
     assert vxfa.supports(d["q"], k32, d["v"], None, d["dst"], c.scale) == vxfa.UNSUPPORTED
+    v32 = vxfa.desc(ADDR, vxfa.F32, d["v"].ne, [4, 4096, 512, 4096 * 64])
+    assert vxfa.supports(d["q"], k32, v32, None, d["dst"], c.scale) == vxfa.OK
     # head dim 96 is a valid op but not one this path implements
     c96 = cases.decode_case(64, hq=4, hkv=1, hd=96, seed=3)
     assert supports(c96) == vxfa.UNSUPPORTED

@@ -78,13 +78,17 @@ SMALL_CASES = [
     lambda: cases.prefill_case(20, hq=4, hkv=1, seed=9, kv_offset=45, capacity=80),
     lambda: cases.prefill_case(25, hq=4, hkv=2, seed=10, causal=False),
     lambda: cases.batched_case(4, hq=8, hkv=2, capacity=96, lo=5, hi=96, seed=11),
+    # F32 K/V: the reference's own cache type and encoder K/V (Q stays F32)
+    lambda: cases.decode_case(120, hq=8, hkv=2, hd=128, seed=12, kv_f32=True),
+    lambda: cases.encoder_case(45, 2, 64, seed=13, kv_f32=True),
+    lambda: cases.prefill_case(30, hq=4, hkv=1, seed=14, kv_offset=9, kv_f32=True),
 ]
 
 
 @pytest.mark.parametrize("make", SMALL_CASES, ids=[f"c{i}" for i in range(len(SMALL_CASES))])
 def test_f64_oracle_matches_torch_sdpa(make):
     c = make()
-    want, live = refmath.sdpa_f64(c, q_f16=True)
+    want, live = refmath.sdpa_f64(c)
     got = cases.oracle_f64(c)
     assert np.allclose(got[live], want[live], rtol=1e-10, atol=1e-12)
     assert (got[~live] == 0).all()   # fully masked rows give zeros (ggml: S == 0 -> 0)
@@ -243,6 +247,31 @@ def test_planted_mistakes_fail_the_check(flag):
     assert float(np.abs(ok - want).max()) <= ATOL
     bad = cases.oracle_ggml(c, flags=flag)
     assert float(np.abs(bad - want).max()) > 10 * ATOL
+
+
+def test_f32_kv_keeps_q_unrounded():
+    """With F32 K ggml keeps Q in F32 (K's dot type): the restatement's and
+    the f64 reference's results then differ from the Q-rounded reference by
+    more than they differ from each other."""
+    c = cases.decode_case(64, hq=4, hkv=1, hd=128, seed=15, kv_f32=True, q_sigma=3.0)
+    exact = cases.oracle_f64(c)
+    rounded = cases.oracle_f64(c, q_f16=True)
+    got = cases.oracle_ggml(c, vkq_f16=False)
+    assert float(np.abs(got - exact).max()) < 1e-5
+    assert float(np.abs(rounded - exact).max()) > 10 * float(np.abs(got - exact).max())
+
+
+@pytest.mark.parametrize("max_bias,softcap", [(8.0, 0.0), (0.0, 30.0)])
+def test_alibi_and_softcap_are_rejected(max_bias, softcap):
+    """voxtral passes 0 for both (src/voxtral.cpp:1611, :1802); the oracle
+    restates neither and reports them as a contract violation."""
+    c = cases.decode_case(16, hq=4, hkv=1, hd=64, seed=33)
+    with pytest.raises(ValueError):
+        oracle.fa_ggml(c.oracle_view("q"), c.oracle_view("k"), c.oracle_view("v"), None, c.scale,
+                       max_bias=max_bias, logit_softcap=softcap)
+    with pytest.raises(ValueError):
+        oracle.fa_f64(c.oracle_view("q"), c.oracle_view("k"), c.oracle_view("v"), None, c.scale,
+                      max_bias=max_bias, logit_softcap=softcap)
 
 
 def test_contract_violation_is_reported():

@@ -25,13 +25,15 @@ struct AttnArgs {
     const _Float16* v;
     const uint16_t* mask; // F16 bits, may be null
     float* dst;           // [B][Nq][Hq][D]
-    float* ws;            // split-KV partials (decode)
+    float* ws;            // split-KV partial records (decode)
+    uint32_t* cnt;        // split-KV arrival counters, one per (batch, kv head); zero between calls
     int64_t q_nb1, q_nb2, q_nb3;   // bytes
     int64_t k_nb1, k_nb2, k_nb3;   // bytes
     int64_t v_nb1, v_nb2, v_nb3;   // bytes
     int64_t m_nb1, m_nb2, m_nb3;   // bytes
     int32_t nq, nkv, hq, hkv, b, bk, hm, bm;
     int32_t q_f16;        // q element type is f16
+    int32_t kv_f32;       // k and v element type is F32 (else f16)
     int32_t n_split;      // decode: workgroups per (batch, kv head)
     int32_t mask_vec;     // mask data and strides 16-byte aligned (128-bit mask loads)
     float scale_log2;     // scale * log2(e)
@@ -329,8 +331,8 @@ __device__ __forceinline__ float pair32_sum(float x) {
 // Host-side launchers (implemented in the kernel translation units).
 namespace vxfa {
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t stream);
-constexpr int kDecodeMaxSplit = 64;
-constexpr int kDecodeWaves = 4;      // wavefronts per decode split workgroup
+constexpr int kDecodeMaxSplit = 32;  // split workgroups per (batch, kv head)
+constexpr int kDecodeWaves = 4;      // wavefronts per decode workgroup
 // Floats per decode partial record: O [G][D], then m [G] and l [G], padded to
 // a multiple of 4 so every record starts 16-byte aligned.
 constexpr int dec_record_floats(int D, int G) { return G * D + ((2 * G + 3) & ~3); }
@@ -338,4 +340,8 @@ hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_
 hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
+// F32 -> f16 copy of a [D, n, H, B] view (byte strides nb1..nb3, rows
+// contiguous) into a contiguous [B][n][H][D] f16 buffer.
+hipError_t launch_to_f16(const float* src, int64_t nb1, int64_t nb2, int64_t nb3, int d, int n, int h, int b,
+                         _Float16* dst, hipStream_t stream);
 }  // namespace vxfa

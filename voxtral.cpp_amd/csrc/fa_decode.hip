@@ -1,36 +1,40 @@
-// fa_decode.hip — single-query (decode-step) attention against an f16 KV
-// cache, split over the KV length, for gfx950.
+// fa_decode.hip — single-query (decode-step) attention against a KV cache,
+// split over the KV length, for gfx950. One launch per call.
 //
 // Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the decode calls
 // voxtral.cpp makes from build_decoder_layer (src/voxtral.cpp:1802) with
 // n_tokens = 1 (step graphs :1959-1962 and :2050-2053), where every KV head
-// serves G = Hq / Hkv query heads (32 / 8 = 4).
+// serves G = Hq / Hkv query heads (32 / 8 = 4). The cache is f16 (the
+// configured layout) or F32 (the reference's own cache type,
+// src/voxtral.cpp:1126-1136); F32 tiles are rounded to f16 as they are
+// loaded for the QK^T product and used as F32 in the P.V product.
 //
-// Two kernels on the caller's stream:
-//   fa_decode_split   grid (n_split * Hkv, B), kDecodeWaves wavefronts per
-//                     workgroup, the kv head fastest-varying (neighbouring
-//                     workgroups stream neighbouring 256-byte head slices of
-//                     the same cache rows). Each workgroup reduces one
-//                     contiguous slice of the live KV range to (O, m, l) per
-//                     query head of its group.
-//   fa_decode_combine grid (Hq * D / 32, B), one wavefront per (query head,
-//                     32 output dims): log-sum-exp merge of the n_split
-//                     partials in a fixed order (deterministic output).
-// With n_split == 1 the split kernel writes the output and no merge runs.
-// The kernel boundary orders the partials' stores before the merge's loads.
-// A merge inside the split kernel by the last workgroup to finish (device-
-// scope stores, an arrival counter, an acquire fence) measured slower: the
-// counter's round trip plus one CU reading all n_split records (its load
-// parallelism caps it near 20-30 GB/s) cost more than the kernel boundary.
+// Grid (n_split * Hkv, B), kDecodeWaves wavefronts per workgroup, the kv head
+// fastest-varying: neighbouring workgroups stream neighbouring head slices of
+// the same cache rows, and with 8 kv heads all splits of one head land on one
+// XCD (workgroups are dealt to the 8 XCDs round robin), so their partial
+// records stay in that XCD's L2. Each workgroup reduces one contiguous slice
+// of the live KV range to (O, m, l) per query head of its group.
 //
-// Inside a wavefront (32-position tiles, software pipelined: the next tile's
-// K/V loads are in flight while the current tile is computed):
+// Merge of the splits, in the same launch: every workgroup stores its partial
+// record, makes it visible device-wide (release fence) and counts itself in
+// on its (batch, kv head) arrival counter; the workgroup that arrives last
+// (acquire fence) merges the n_split records in a fixed order — the output
+// does not depend on arrival order — writes the output and sets the counter
+// back to zero. Counters are zero when the context is created and every
+// launch leaves them at zero. With n_split == 1 the workgroup writes the
+// output directly.
+//
+// Inside a wavefront (tiles of TP positions, 32 for f16 and 16 for F32 K/V,
+// so a tile is 16 KB either way; software pipelined: the next tile's K/V
+// loads are in flight while the current tile is computed):
 //   QK^T  v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims). The A operand
 //         holds the G query heads replicated 16/G times, so every lane gets
 //         the scores of all G heads for one position: no cross-lane dot
 //         reduction.
 //   K     loaded from HBM straight into the MFMA B-operand layout
-//         (16 positions x 64 contiguous bytes per 128-bit load instruction).
+//         (16 positions x 64 contiguous bytes per 128-bit load instruction,
+//         128 bytes as two loads for F32).
 //   V     16 (hd128) or 8 (hd64) lanes per row, fully coalesced 128-bit
 //         loads; P.V on the VALU with fp32 accumulators (each lane owns 8
 //         dims of all G heads); P is handed from the MFMA layout to the V
@@ -45,28 +49,117 @@
 // it, so no scan runs.
 #include "fa_common.h"
 
+#include <type_traits>
+
 namespace vxfa {
 
 constexpr int DEC_WAVES = kDecodeWaves;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
-constexpr int DEC_TILE = 32;
 
-template <int D, int G, bool QF16, bool MASK>
-__global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
+// Log-sum-exp merge of the n_split partial records of one (batch, kv head)
+// (its G query heads), run by the workgroup that arrived last:
+//   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
+// The O partials are loaded first (their addresses do not depend on the
+// weights; loads past the last split read the last record again, so all of
+// them issue back to back), then wavefront 0 loads the n_split (m, l) pairs,
+// one split per lane, and forms the weights with wavefront reductions: one
+// memory round trip. The summation order is fixed: the output is
+// deterministic.
+template <int D, int G>
+__device__ __forceinline__ void merge_records(const AttnArgs& a, const float* base, int b, int g,
+                                              float (*cw)[kDecodeMaxSplit], float* cl, floatx4* cpart) {
+    constexpr int NF4 = G * D / 4;                              // float4 per record's O block
+    constexpr int NGRP = DEC_THREADS / NF4;                     // split groups
+    constexpr int MAXS = (kDecodeMaxSplit + NGRP - 1) / NGRP;   // splits per thread
+    constexpr int RS = dec_record_floats(D, G);
+    static_assert(NGRP * NF4 == DEC_THREADS, "merge split");
+    static_assert(kDecodeMaxSplit <= 64, "one (m, l) pair per lane of wavefront 0");
+    static_assert(RS % 4 == 0, "16-byte aligned records");
+    const int tid = threadIdx.x;
+    const int ns = a.n_split;
+    const int f = tid % NF4, grp = tid / NF4;
+    const int h = f / (D / 4);
+
+    floatx4 o[MAXS];
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+        const int sp = min(grp + i * NGRP, ns - 1);
+        o[i] = *(const floatx4*)(base + (int64_t)sp * RS + 4 * f);
+    }
+    if (tid < 64) {
+        const float* r = base + (int64_t)min(tid, ns - 1) * RS + G * D;
+        float m[G], l[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            m[j] = r[j];
+            l[j] = r[G + j];
+        }
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            m[j] = tid < ns ? m[j] : -INFINITY;
+            l[j] = tid < ns ? l[j] : 0.f;
+            float M = m[j];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+            const float Ms = (M == -INFINITY) ? 0.f : M;
+            const float w = exp2_fast(m[j] - Ms);   // 0 for an empty split (m = -inf)
+            float L = w * l[j];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
+            if (tid < kDecodeMaxSplit) cw[j][tid] = w;
+            if (tid == 0) cl[j] = L;
+        }
+    }
+    __syncthreads();
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+        const int sp = grp + i * NGRP;
+        const float w = sp < ns ? cw[h][sp] : 0.f;
+        acc[0] = fmaf(w, o[i][0], acc[0]);
+        acc[1] = fmaf(w, o[i][1], acc[1]);
+        acc[2] = fmaf(w, o[i][2], acc[2]);
+        acc[3] = fmaf(w, o[i][3], acc[3]);
+    }
+    cpart[grp * NF4 + f] = acc;
+    __syncthreads();
+    if (tid < NF4) {
+        floatx4 s = cpart[tid];
+#pragma unroll
+        for (int p = 1; p < NGRP; ++p) {
+            const floatx4 y = cpart[p * NF4 + tid];
+            s[0] += y[0]; s[1] += y[1]; s[2] += y[2]; s[3] += y[3];
+        }
+        const float L = cl[tid / (D / 4)];
+        const float inv = (L == 0.f) ? 0.f : 1.0f / L;
+        const floatx4 out = {s[0] * inv, s[1] * inv, s[2] * inv, s[3] * inv};
+        *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G) * D + 4 * tid) = out;
+    }
+}
+
+template <int D, int G, bool QF16, bool MASK, bool KV32>
+__global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     static_assert(D == 64 || D == 128, "head dim");
     static_assert(G == 1 || G == 2 || G == 4, "GQA group");
     constexpr int KS = D / 32;        // MFMA k-steps of 32 dims
-    constexpr int CH = D / 8;         // 16-byte chunks per row = PV lanes per row
-    constexpr int RPI = 64 / CH;      // rows covered by one PV load instruction
-    constexpr int NV = DEC_TILE / RPI;
+    constexpr int TP = KV32 ? 16 : 32;   // positions per tile (16 KB of K and V either way)
+    constexpr int NG = TP / 16;       // 16-position MFMA groups per tile
+    constexpr int CH = D / 8;         // lanes per V row (8 dims each)
+    constexpr int RPI = 64 / CH;      // V rows covered by one load instruction
+    constexpr int NV = TP / RPI;
+    constexpr int ESZ = KV32 ? 4 : 2; // K/V element size
 
-    __shared__ floatx4 lds_p[DEC_WAVES][DEC_TILE];
+    __shared__ floatx4 lds_p[DEC_WAVES][TP];
     __shared__ float lds_acc[DEC_WAVES][G][D];
     __shared__ float lds_m[DEC_WAVES][G];
     __shared__ float lds_l[DEC_WAVES][G];
     __shared__ int lds_red[2 * DEC_WAVES];
     __shared__ half8 lds_q[G * D / 8];   // the group's query heads, f16, [G][D]
     __shared__ float2 lds_rope[D / 2];   // cos / sin of each pair's rotary angle (with rope_pos)
+    __shared__ float lds_cw[G][kDecodeMaxSplit];
+    __shared__ float lds_cl[G];
+    __shared__ floatx4 lds_cpart[DEC_THREADS];
+    __shared__ int lds_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -75,6 +168,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     const int split = blockIdx.x / a.hkv;
     const int b = blockIdx.y;
     const int bkv = b / (a.b / a.bk);
+    const int pair = b * a.hkv + g;
     constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
     // rotary position of the query token (also the appended row's: the host
     // requires one kv batch per q batch), requested before any other load. A
@@ -122,7 +216,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     const bool new_live = a.append && hi == a.nkv;
     const int hi_main = a.append ? min(hi, a.nkv - 1) : hi;
     const int span = max(hi_main - lo, 0);
-    const int ntiles = (span + DEC_TILE - 1) / DEC_TILE;
+    const int ntiles = (span + TP - 1) / TP;
     const int t_begin = (int)(((int64_t)ntiles * split) / a.n_split);
     const int t_end = (int)(((int64_t)ntiles * (split + 1)) / a.n_split);
 
@@ -142,10 +236,37 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     const int vrow = lane / CH;           // row offset owned in the V layout
     const int vcol = (lane % CH) * 8;     // dims owned in the V layout
 
-    struct Tile {
-        half8 k[2][KS];
+    // One tile in registers: K in the MFMA B-operand layout (position
+    // 16 grp + lane % 16, dims 32 ks + kcol .. + 7), V in the P.V layout (row
+    // vrow + RPI i, dims vcol .. vcol + 7), mask entries of the lane's
+    // position for its four accumulator rows.
+    struct TileH {
+        half8 k[NG][KS];
         half8 v[NV];
-        uint16_t m[2][4];
+        uint16_t m[NG][4];
+    };
+    struct TileF {
+        floatx4 k[NG][KS][2];
+        floatx4 v[NV][2];
+        uint16_t m[NG][4];
+    };
+    using Tile = std::conditional_t<KV32, TileF, TileH>;
+    auto kop = [&](const Tile& T, int grp, int ks) -> half8 {
+        if constexpr (KV32) {
+            half8 r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                r[e] = (_Float16)T.k[grp][ks][0][e];
+                r[4 + e] = (_Float16)T.k[grp][ks][1][e];
+            }
+            return r;
+        } else {
+            return T.k[grp][ks];
+        }
+    };
+    auto vval = [&](const Tile& T, int i, int j) -> float {
+        if constexpr (KV32) return T.v[i][j >> 2][j & 3];
+        else return (float)T.v[i][j];
     };
     // cache row of logical position pos: pos itself, or in a ring of
     // ring_cap rows starting at ring_start, (ring_start + pos) mod ring_cap
@@ -155,14 +276,21 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         return r >= a.ring_cap ? r - a.ring_cap : r;
     };
     auto load_tile = [&](Tile& T, int t) {
-        const int p0 = lo + t * DEC_TILE;
-        const int pend = min(p0 + DEC_TILE, hi_main);
+        const int p0 = lo + t * TP;
+        const int pend = min(p0 + TP, hi_main);
 #pragma unroll
-        for (int grp = 0; grp < 2; ++grp) {
+        for (int grp = 0; grp < NG; ++grp) {
             const int pos = max(min(p0 + 16 * grp + (lane & 15), pend - 1), 0);
-            const char* kp = kb + (int64_t)row_of(pos) * a.k_nb1 + kcol * 2;
+            const char* kp = kb + (int64_t)row_of(pos) * a.k_nb1 + kcol * ESZ;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
+            for (int ks = 0; ks < KS; ++ks) {
+                if constexpr (KV32) {
+                    T.k[grp][ks][0] = *(const floatx4*)(kp + 128 * ks);
+                    T.k[grp][ks][1] = *(const floatx4*)(kp + 128 * ks + 16);
+                } else {
+                    T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
+                }
+            }
             if constexpr (masked) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) T.m[grp][i] = mplane[i][pos];
@@ -171,18 +299,25 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int pos = max(min(p0 + vrow + i * RPI, pend - 1), 0);
-            T.v[i] = *(const half8*)(vb + (int64_t)row_of(pos) * a.v_nb1 + vcol * 2);
+            const char* vp = vb + (int64_t)row_of(pos) * a.v_nb1 + vcol * ESZ;
+            if constexpr (KV32) {
+                T.v[i][0] = *(const floatx4*)(vp);
+                T.v[i][1] = *(const floatx4*)(vp + 16);
+            } else {
+                T.v[i] = *(const half8*)(vp);
+            }
         }
     };
 
     // ---- prologue: Q and the first tile go out together -------------------
     // The group's G query heads (G * D elements, contiguous per head) are read
     // once per workgroup, 8 elements per thread, rounded to f16 (ggml's Q
-    // conversion before an f16 K dot product) and staged in LDS; each
-    // wavefront then reads its MFMA A operand (head (lane & 15) % G, dims
-    // 32 ks + 8 (lane >> 4) .. + 7) from there. (The Q element type is a
-    // template parameter: a load-or-convert branch on it makes the compiler
-    // wait for all global loads inside the KV loop.)
+    // conversion before an f16 K dot product; the MFMA product needs it for
+    // F32 K too) and staged in LDS; each wavefront then reads its MFMA A
+    // operand (head (lane & 15) % G, dims 32 ks + 8 (lane >> 4) .. + 7) from
+    // there. (The Q element type is a template parameter: a load-or-convert
+    // branch on it makes the compiler wait for all global loads inside the KV
+    // loop.)
     constexpr int QCH = QF16 ? 1 : 2;                // 16-byte loads per 8 elements
     constexpr int QTHREADS = G * D / 8;              // threads holding 8 Q elements
     static_assert(QTHREADS <= DEC_THREADS, "Q staging");
@@ -244,18 +379,18 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
 
     auto process = [&](const Tile& T, int p0, int pend) {
-        floatx4 sc[2];
+        floatx4 sc[NG];
 #pragma unroll
-        for (int grp = 0; grp < 2; ++grp) {
+        for (int grp = 0; grp < NG; ++grp) {
             sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], T.k[grp][ks], sc[grp], 0, 0, 0);
+                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kop(T, grp, ks), sc[grp], 0, 0, 0);
         }
         // scores in log2 units; lane holds head (i % G) at position p0 + 16*grp + (lane & 15)
-        float x[2][4];
+        float x[NG][4];
 #pragma unroll
-        for (int grp = 0; grp < 2; ++grp) {
+        for (int grp = 0; grp < NG; ++grp) {
             const bool valid = p0 + 16 * grp + (lane & 15) < pend;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -267,21 +402,29 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
                 x[grp][i] = valid ? xv : -INFINITY;
             }
         }
-        float alpha[4], p[2][4];
+        float alpha[4], p[NG][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float mx = row16_max(fmaxf(x[0][i], x[1][i]));
+            float mx = x[0][i];
+#pragma unroll
+            for (int grp = 1; grp < NG; ++grp) mx = fmaxf(mx, x[grp][i]);
+            mx = row16_max(mx);
             const float mnew = fmaxf(m_run[i], mx);
             const float msafe = (mnew == -INFINITY) ? 0.f : mnew;
             alpha[i] = exp2_fast(m_run[i] - msafe);
-            p[0][i] = exp2_fast(x[0][i] - msafe);
-            p[1][i] = exp2_fast(x[1][i] - msafe);
-            l_run[i] = fmaf(l_run[i], alpha[i], p[0][i] + p[1][i]);
+            float ps = 0.f;
+#pragma unroll
+            for (int grp = 0; grp < NG; ++grp) {
+                p[grp][i] = exp2_fast(x[grp][i] - msafe);
+                ps += p[grp][i];
+            }
+            l_run[i] = fmaf(l_run[i], alpha[i], ps);
             m_run[i] = mnew;
         }
         if ((lane >> 4) == 0) {
-            lds_p[wave][lane] = floatx4{p[0][0], p[0][1], p[0][2], p[0][3]};
-            lds_p[wave][16 + lane] = floatx4{p[1][0], p[1][1], p[1][2], p[1][3]};
+#pragma unroll
+            for (int grp = 0; grp < NG; ++grp)
+                lds_p[wave][16 * grp + lane] = floatx4{p[grp][0], p[grp][1], p[grp][2], p[grp][3]};
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -294,7 +437,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
 #pragma unroll
             for (int h = 0; h < G; ++h)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pv[h], (float)T.v[i][j], acc[h][j]);
+                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pv[h], vval(T, i, j), acc[h][j]);
         }
         __builtin_amdgcn_wave_barrier();
     };
@@ -303,12 +446,12 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     while (t < t_end) {
         int tn = t + DEC_WAVES;
         if (tn < t_end) load_tile(TB, tn);
-        process(TA, lo + t * DEC_TILE, min(lo + t * DEC_TILE + DEC_TILE, hi_main));
+        process(TA, lo + t * TP, min(lo + t * TP + TP, hi_main));
         t = tn;
         if (t >= t_end) break;
         tn = t + DEC_WAVES;
         if (tn < t_end) load_tile(TA, tn);
-        process(TB, lo + t * DEC_TILE, min(lo + t * DEC_TILE + DEC_TILE, hi_main));
+        process(TB, lo + t * TP, min(lo + t * TP + TP, hi_main));
         t = tn;
     }
 
@@ -317,51 +460,54 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     // positions of the one-row tile clamp to it; only position n_kv - 1 is
     // valid in process()), rounded to f16 exactly as the cache will hold it.
     // The lanes holding each element once write the rounded row to the cache.
-    if (a.append && split == a.n_split - 1 && wave == 0) {
-        const int pn = a.nkv - 1;
-        const float* kn = (const float*)((const char*)a.k_new + (int64_t)bkv * a.kn_nb3) + g * D;
-        const float* vn = (const float*)((const char*)a.v_new + (int64_t)bkv * a.vn_nb3) + g * D;
-        // every load of the row first (one round trip), then rotation (K, with
-        // rope_pos; the table holds the row's angles) and rounding
-        floatx4 kr[KS][2], vr[2];
+    // (f16 caches only; the host rejects an append to an F32 cache.)
+    if constexpr (!KV32) {
+        if (a.append && split == a.n_split - 1 && wave == 0) {
+            const int pn = a.nkv - 1;
+            const float* kn = (const float*)((const char*)a.k_new + (int64_t)bkv * a.kn_nb3) + g * D;
+            const float* vn = (const float*)((const char*)a.v_new + (int64_t)bkv * a.vn_nb3) + g * D;
+            // every load of the row first (one round trip), then rotation (K,
+            // with rope_pos; the table holds the row's angles) and rounding
+            floatx4 kr[KS][2], vr[2];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            kr[ks][0] = *(const floatx4*)(kn + kcol + 32 * ks);
-            kr[ks][1] = *(const floatx4*)(kn + kcol + 32 * ks + 4);
+            for (int ks = 0; ks < KS; ++ks) {
+                kr[ks][0] = *(const floatx4*)(kn + kcol + 32 * ks);
+                kr[ks][1] = *(const floatx4*)(kn + kcol + 32 * ks + 4);
+            }
+            vr[0] = *(const floatx4*)(vn + vcol);
+            vr[1] = *(const floatx4*)(vn + vcol + 4);
+            auto cvt8 = [&](const floatx4 (&r)[2], int d0, bool rot) {
+                float x[8] = {r[0][0], r[0][1], r[0][2], r[0][3], r[1][0], r[1][1], r[1][2], r[1][3]};
+                if (rot) rope8_tab(x, d0, lds_rope, a.rope_dims);
+                half8 y;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) y[i] = (_Float16)x[i];
+                return y;
+            };
+            const bool rot = a.rope_pos != nullptr;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 kx = cvt8(kr[ks], kcol + 32 * ks, rot);
+#pragma unroll
+                for (int grp = 0; grp < NG; ++grp) TA.k[grp][ks] = kx;
+            }
+            const half8 vx = cvt8(vr, vcol, false);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) TA.v[i] = vx;
+            if constexpr (masked) {
+#pragma unroll
+                for (int grp = 0; grp < NG; ++grp)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) TA.m[grp][i] = mplane[i][pn];
+            }
+            if (new_live) process(TA, pn, pn + 1);
+            if ((lane & 15) == 0) {
+                _Float16* kc = (_Float16*)(kb + (int64_t)row_of(pn) * a.k_nb1) + kcol;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) *(half8*)(kc + 32 * ks) = TA.k[0][ks];
+            }
+            if (lane < CH) *(half8*)((_Float16*)(vb + (int64_t)row_of(pn) * a.v_nb1) + vcol) = vx;
         }
-        vr[0] = *(const floatx4*)(vn + vcol);
-        vr[1] = *(const floatx4*)(vn + vcol + 4);
-        auto cvt8 = [&](const floatx4 (&r)[2], int d0, bool rot) {
-            float x[8] = {r[0][0], r[0][1], r[0][2], r[0][3], r[1][0], r[1][1], r[1][2], r[1][3]};
-            if (rot) rope8_tab(x, d0, lds_rope, a.rope_dims);
-            half8 y;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) y[i] = (_Float16)x[i];
-            return y;
-        };
-        const bool rot = a.rope_pos != nullptr;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const half8 kx = cvt8(kr[ks], kcol + 32 * ks, rot);
-            TA.k[0][ks] = kx;
-            TA.k[1][ks] = kx;
-        }
-        const half8 vx = cvt8(vr, vcol, false);
-#pragma unroll
-        for (int i = 0; i < NV; ++i) TA.v[i] = vx;
-        if constexpr (masked) {
-#pragma unroll
-            for (int grp = 0; grp < 2; ++grp)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) TA.m[grp][i] = mplane[i][pn];
-        }
-        if (new_live) process(TA, pn, pn + 1);
-        if ((lane & 15) == 0) {
-            _Float16* kc = (_Float16*)(kb + (int64_t)row_of(pn) * a.k_nb1) + kcol;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) *(half8*)(kc + 32 * ks) = TA.k[0][ks];
-        }
-        if (lane < CH) *(half8*)((_Float16*)(vb + (int64_t)row_of(pn) * a.v_nb1) + vcol) = vx;
     }
 
     // ---- merge lanes, then wavefronts ------------------------------------
@@ -389,9 +535,8 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
     }
     __syncthreads();
 
-    float* rec = nullptr;
-    if (a.n_split > 1)
-        rec = a.ws + ((int64_t)(b * a.hkv + g) * a.n_split + split) * dec_record_floats(D, G);
+    constexpr int RS = dec_record_floats(D, G);
+    float* rec = a.n_split > 1 ? a.ws + ((int64_t)pair * a.n_split + split) * RS : nullptr;
     for (int o = tid; o < G * D; o += DEC_THREADS) {
         const int h = o / D, d = o % D;
         float M = lds_m[0][h];
@@ -412,92 +557,45 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode_split(AttnArgs a) {
             if (d == 0) { rec[G * D + h] = M; rec[G * D + G + h] = L; }
         }
     }
+    if (rec == nullptr) return;
+
+    // ---- split merge by the last workgroup of this (batch, kv head) ---------
+    __threadfence();   // release: this workgroup's record before its count
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = atomicAdd(a.cnt + pair, 1u);
+        lds_last = prev == (uint32_t)(a.n_split - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!lds_last) return;
+    __threadfence();   // acquire: every other record is visible
+    merge_records<D, G>(a, a.ws + (int64_t)pair * a.n_split * RS, b, g, lds_cw, lds_cl, lds_cpart);
+    if (tid == 0) atomicExch(a.cnt + pair, 0u);   // ready for the next call
 }
 
-// Log-sum-exp merge of the n_split partial records, one wavefront per
-// (query head, 32 output dims):
-//   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
-// Lane (f, grp) loads float4 f of the slice from splits grp, grp + 8, ...
-// while lane s loads split s's (m, l); all loads issue back to back (loads
-// past the last split read the last record again; their weights are zero), so
-// the merge costs one memory round trip. Wavefront reductions form the
-// weights and the sums, in a fixed order: the output is deterministic.
-template <int D, int G>
-__global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
-    constexpr int CSUB = D / 32;                  // 32-dim slices per head
-    constexpr int CF4 = 8;                        // float4 per slice
-    constexpr int NGRP = 64 / CF4;                // split groups
-    constexpr int MAXS = kDecodeMaxSplit / NGRP;  // splits per lane
-    constexpr int RS = dec_record_floats(D, G);
-    static_assert(kDecodeMaxSplit == 64, "one (m, l) pair per lane");
-    const int lane = threadIdx.x;
-    const int hq = blockIdx.x / CSUB, sl = blockIdx.x % CSUB;
-    const int g = hq / G, h = hq % G;
-    const int b = blockIdx.y;
-    const int ns = a.n_split;
-    const float* base = a.ws + (int64_t)(b * a.hkv + g) * ns * RS;
-    const int f = lane % CF4, grp = lane / CF4;
-
-    floatx4 o[MAXS];
-#pragma unroll
-    for (int i = 0; i < MAXS; ++i) {
-        const int sp = min(grp + i * NGRP, ns - 1);
-        o[i] = *(const floatx4*)(base + (int64_t)sp * RS + h * D + 32 * sl + 4 * f);
+template <int D, int G, bool KV32>
+static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
+    const dim3 grid(a.n_split * a.hkv, a.b), block(DEC_THREADS);
+    if (a.mask) {
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32>), grid, block, 0, st, a);
+    } else {
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32>), grid, block, 0, st, a);
     }
-    const float* r = base + (int64_t)min(lane, ns - 1) * RS + G * D;
-    float m = r[h], l = r[G + h];
-    m = lane < ns ? m : -INFINITY;
-    l = lane < ns ? l : 0.f;
-    float M = m;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-    const float Ms = (M == -INFINITY) ? 0.f : M;
-    const float w = exp2_fast(m - Ms);            // 0 for an empty split (m = -inf)
-    float L = w * l;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
-
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < MAXS; ++i) {
-        const int sp = grp + i * NGRP;
-        const float ws = __shfl(w, sp & 63, 64);
-        const float wt = sp < ns ? ws : 0.f;
-        acc[0] = fmaf(wt, o[i][0], acc[0]);
-        acc[1] = fmaf(wt, o[i][1], acc[1]);
-        acc[2] = fmaf(wt, o[i][2], acc[2]);
-        acc[3] = fmaf(wt, o[i][3], acc[3]);
-    }
-#pragma unroll
-    for (int off = CF4; off < 64; off <<= 1)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] += shfl_xor(acc[c], off);
-    if (grp == 0) {
-        const float inv = (L == 0.f) ? 0.f : 1.0f / L;
-        const floatx4 out = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-        *(floatx4*)(a.dst + ((int64_t)b * a.hq + hq) * D + 32 * sl + 4 * f) = out;
-    }
+    return hipGetLastError();
 }
 
 template <int D, int G>
 static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
-    if (a.b > 65535) return hipErrorInvalidValue;
-    const dim3 grid(a.n_split * a.hkv, a.b), block(DEC_THREADS);
-    if (a.mask) {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode_split<D, G, true, true>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((fa_decode_split<D, G, false, true>), grid, block, 0, st, a);
-    } else {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode_split<D, G, true, false>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((fa_decode_split<D, G, false, false>), grid, block, 0, st, a);
-    }
-    if (a.n_split > 1)
-        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G * (D / 32), a.b), dim3(64), 0, st, a);
-    return hipGetLastError();
+    return a.kv_f32 ? launch_dgk<D, G, true>(a, st) : launch_dgk<D, G, false>(a, st);
 }
 
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t st) {
     if (a.n_split < 1 || a.n_split > kDecodeMaxSplit) return hipErrorInvalidValue;
-    if (a.n_split > 1 && a.ws == nullptr) return hipErrorInvalidValue;
+    if (a.n_split > 1 && (a.ws == nullptr || a.cnt == nullptr)) return hipErrorInvalidValue;
+    if (a.b > 65535 || (int64_t)a.n_split * a.hkv > 0x7fffffff) return hipErrorInvalidValue;
+    if (a.kv_f32 && a.append) return hipErrorInvalidValue;
     if (head_dim == 128) {
         if (group == 4) return launch_dg<128, 4>(a, st);
         if (group == 2) return launch_dg<128, 2>(a, st);
@@ -519,6 +617,44 @@ hipError_t launch_zero(float* dst, int64_t n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, n);
+    return hipGetLastError();
+}
+
+// F32 -> f16 (round to nearest even) copy of the view src [d, n, h, b] into a
+// contiguous [b][n][h][d] buffer: one thread per 8 elements (two 16-byte
+// loads, one 16-byte store). Used to stage F32 K/V for the prefill kernels.
+__global__ __launch_bounds__(256) void to_f16_kernel(const float* src, int64_t nb1, int64_t nb2, int64_t nb3, int d,
+                                                     int n, int h, int64_t total8, _Float16* dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total8) return;
+    const int c8 = d / 8;
+    int64_t r = i / c8;
+    const int e = (int)(i - r * c8) * 8;
+    const int hh = (int)(r % h);
+    r /= h;
+    const int pos = (int)(r % n);
+    const int bb = (int)(r / n);
+    const floatx4* p = (const floatx4*)((const char*)src + (int64_t)pos * nb1 + (int64_t)hh * nb2 + (int64_t)bb * nb3) +
+                       e / 4;
+    const floatx4 x0 = p[0], x1 = p[1];
+    half8 y;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        y[j] = (_Float16)x0[j];
+        y[4 + j] = (_Float16)x1[j];
+    }
+    *(half8*)(dst + i * 8) = y;
+}
+
+hipError_t launch_to_f16(const float* src, int64_t nb1, int64_t nb2, int64_t nb3, int d, int n, int h, int b,
+                         _Float16* dst, hipStream_t st) {
+    if (d % 8 || n < 0 || h < 0 || b < 0) return hipErrorInvalidValue;
+    const int64_t total8 = (int64_t)b * n * h * (d / 8);
+    if (total8 == 0) return hipSuccess;
+    const int64_t blocks = (total8 + 255) / 256;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, st, src, nb1, nb2, nb3, d, n, h, total8,
+                       dst);
     return hipGetLastError();
 }
 

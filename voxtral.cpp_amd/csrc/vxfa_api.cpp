@@ -19,10 +19,20 @@
 #include "../../include/vxfa.h"
 #include "fa_common.h"
 
+// Device workspace of a context, allocated once by vxfa_ctx_create (no call
+// allocates, frees or synchronises): the split-KV arrival counters (zeroed at
+// creation; every launch leaves them at zero), the split-KV partial records,
+// and f16 staging for F32 K/V of prefill calls.
+constexpr size_t kCounterSlots = 65536;                 // (batch, kv head) pairs with a split merge
+constexpr size_t kRecordBytes = (size_t)18 << 20;       // 256 pairs x 32 splits of G = 4, hd 128
+constexpr size_t kStageBytes = (size_t)32 << 20;        // F32 K and V of 8192 rows x 1024 as f16
+
 struct vxfa_ctx {
     int device = 0;
-    float* ws = nullptr;
-    size_t ws_floats = 0;
+    char* ws = nullptr;           // one device allocation holding the three regions
+    uint32_t* cnt = nullptr;      // kCounterSlots arrival counters
+    float* rec = nullptr;         // kRecordBytes of partial records
+    _Float16* stage = nullptr;    // kStageBytes of f16 K/V staging
     char last_error[256] = {0};
     // launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
     // VXFA_PREFILL_WAVES), read once when the context is created; 0 = heuristic
@@ -87,7 +97,9 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
         return VXFA_INVALID_ARG;
     }
     // what this path implements
-    if (k->type != VXFA_TYPE_F16 || v->type != VXFA_TYPE_F16) { *why = "k and v must be F16"; return VXFA_UNSUPPORTED; }
+    // K/V: f16 (the configured cache) or F32 (the reference's own cache,
+    // src/voxtral.cpp:1126-1136, and the encoder's mul_mat outputs, :1581-1605)
+    if (k->type != v->type) { *why = "k and v must have one type"; return VXFA_UNSUPPORTED; }
     if (mask && mask->type != VXFA_TYPE_F16) { *why = "mask must be F16"; return VXFA_UNSUPPORTED; }
     if (dst->type != VXFA_TYPE_F32) { *why = "dst must be F32"; return VXFA_UNSUPPORTED; }
     if (dst->nb[0] != 4 || dst->nb[1] != 4 * (size_t)dst->ne[0] || dst->nb[2] != dst->nb[1] * (size_t)dst->ne[1] ||
@@ -127,12 +139,6 @@ int check(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, cons
     return VXFA_OK;
 }
 
-// Workgroups per (batch, kv head) for the decode split kernel: 2048
-// wavefronts in all (8 per CU), at least 64 live positions per workgroup
-// (two of its wavefronts busy: more, smaller splits finish sooner when the
-// range is short), and at most kDecodeMaxSplit so the merge stays short.
-// With a mask tensor every split workgroup scans the whole mask row, so the
-// caller caps the count (measured on a 2048 window of a 16K cache).
 // New K/V rows for an append: F32 [Hkv * D, n_new, 1, Bk] with contiguous
 // 16-byte-aligned rows, going to the last n_new rows of the F16 cache views
 // k, v [D, n_kv, Hkv, Bk] (checked by check()).
@@ -189,14 +195,30 @@ vxfa::AppendArgs append_args(const vxfa_tensor* k, const vxfa_tensor* v, const v
     return a;
 }
 
+// Workgroups per (batch, kv head) for the decode split kernel: 2048
+// wavefronts in all (8 per CU), at least 64 live positions per workgroup
+// (two of its wavefronts busy: more, smaller splits finish sooner when the
+// range is short), and at most kDecodeMaxSplit so the merge stays short.
+// With a mask tensor every split workgroup scans the whole mask row, so the
+// caller caps the count (measured on a 2048 window of a 16K cache).
 int choose_split(int64_t pairs, int64_t nkv) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
     const int64_t by_len = (nkv + 63) / 64;
     if (s > by_len) s = by_len;
-    if (s > 64) s = 64;
+    if (s > vxfa::kDecodeMaxSplit) s = vxfa::kDecodeMaxSplit;
     if (s < 1) s = 1;
     return (int)s;
+}
+
+// The split count the context's workspace can hold: pairs * S records of
+// rec_floats each, and one arrival counter per pair (else no split).
+int fit_split(int S, int64_t pairs, int rec_floats) {
+    if (S <= 1) return 1;
+    if (pairs > (int64_t)kCounterSlots) return 1;
+    const int64_t cap = (int64_t)(kRecordBytes / sizeof(float)) / (pairs * rec_floats);
+    if (cap < 2) return 1;
+    return S < cap ? S : (int)cap;
 }
 
 }  // namespace
@@ -213,6 +235,23 @@ vxfa_ctx* vxfa_ctx_create(int device) {
     if (const char* e = getenv("VXFA_PREFILL_WAVES")) c->waves_override = atoi(e);
     if (const char* e = getenv("VXFA_PREFILL_PP")) c->pp_enabled = atoi(e) != 0;
     if (const char* e = getenv("VXFA_PP_SHAPE")) c->pp_shape = atoi(e);
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    const size_t cnt_bytes = kCounterSlots * sizeof(uint32_t);
+    const size_t total = cnt_bytes + kRecordBytes + kStageBytes;
+    bool ok = hipSetDevice(device) == hipSuccess && hipMalloc(&c->ws, total) == hipSuccess;
+    // the counters start at zero; the synchronisation makes that so before any
+    // call (a call may be captured into a graph, so it must not clear them)
+    ok = ok && hipMemset(c->ws, 0, cnt_bytes) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+    (void)hipSetDevice(prev);
+    if (!ok) {
+        if (c->ws) (void)hipFree(c->ws);
+        delete c;
+        return nullptr;
+    }
+    c->cnt = reinterpret_cast<uint32_t*>(c->ws);
+    c->rec = reinterpret_cast<float*>(c->ws + cnt_bytes);
+    c->stage = reinterpret_cast<_Float16*>(c->ws + cnt_bytes + kRecordBytes);
     return c;
 }
 
@@ -293,6 +332,9 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
         } else if (q->ne[1] != 1 || !(G == 1 || G == 2 || G == 4) || mask || (k_new && k_new->ne[1] != 1)) {
             why = "ring: single-token decode (GQA group 1, 2 or 4) without a mask, at most one new row";
             rc = VXFA_UNSUPPORTED;
+        } else if (k->type != VXFA_TYPE_F16) {
+            why = "ring: f16 cache only";
+            rc = VXFA_UNSUPPORTED;
         }
     }
     if (rc != VXFA_OK) {
@@ -347,6 +389,7 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     a.hm = mask ? (int32_t)mask->ne[2] : 1;
     a.bm = mask ? (int32_t)mask->ne[3] : 1;
     a.q_f16 = q->type == VXFA_TYPE_F16;
+    a.kv_f32 = k->type == VXFA_TYPE_F32;
     a.mask_vec = mask && aligned16(mask->data, 0) && !(mask->nb[1] & 15) && !(mask->nb[2] & 15) &&
                  !(mask->nb[3] & 15);
     a.scale_log2 = scale * vxfa::kLog2e;
@@ -391,46 +434,59 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
         if (mask && B > 1) {
             // streams of ragged lengths (a mask row each): the longest sets the
             // time, so split every stream finer, about 2048 workgroups in all
-            // (32 streams x 8 kv heads: 8 splits, 139 us against 149 with 2)
             const int64_t s2 = (2048 + B * Hkv - 1) / (B * Hkv);
             if (s2 > S) S = (int)(s2 < (Nkv + 63) / 64 ? s2 : (Nkv + 63) / 64);
         }
         if (mask && S > kMaskedSplitCap) S = kMaskedSplitCap;
-        if (c->split_override > 0) S = c->split_override < vxfa::kDecodeMaxSplit ? c->split_override : vxfa::kDecodeMaxSplit;
+        if (c->split_override > 0) S = c->split_override;
+        if (S > vxfa::kDecodeMaxSplit) S = vxfa::kDecodeMaxSplit;
+        S = fit_split(S, B * Hkv, vxfa::dec_record_floats((int)D, (int)G));
         a.n_split = S;
-        if (S > 1) {
-            const size_t need = (size_t)(B * Hkv) * S * vxfa::dec_record_floats((int)D, (int)G);
-            if (need > c->ws_floats) {
-                // grow: work queued earlier on this stream may still read the old buffer
-                if (c->ws) {
-                    (void)hipStreamSynchronize(st);
-                    (void)hipFree(c->ws);
-                }
-                c->ws = nullptr;
-                c->ws_floats = 0;
-                if (hipMalloc(&c->ws, need * sizeof(float)) != hipSuccess) {
-                    c->ws = nullptr;
-                    set_err(c, "workspace allocation of %zu bytes failed", need * sizeof(float));
-                    return VXFA_NO_WORKSPACE;
-                }
-                c->ws_floats = need;
-            }
-            a.ws = c->ws;
-        }
+        a.ws = c->rec;
+        a.cnt = c->cnt;
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
-    } else if (D == 64 && !mask && !implicit && !rope && scale != 0.0f && c->pp_enabled) {
-        // (scale 0 goes to the general kernel: the pipelined one folds the
-        // scale into the exponent and scores the partial block's dead rows -inf)
-        // encoder prefill: the software-pipelined hd 64 kernel
-        e = vxfa::launch_prefill64_pp(a, c->pp_shape, st);
     } else {
-        // query-row wavefronts per workgroup (each with its KV partner
-        // wavefronts): 4 shares every staged K/V step among 128 query rows;
-        // hd 128 and small grids (fewer than 128 workgroups of 128 rows) use 2
-        const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
-        int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
-        if (c->waves_override == 2 || c->waves_override == 4) waves = c->waves_override;
-        e = vxfa::launch_prefill(a, (int)D, waves, st);
+        if (a.kv_f32) {
+            // F32 K/V (the reference's own cache and encoder K/V): an f16 copy
+            // in the context's staging area, [Bk][Nkv][Hkv][D], read by the
+            // prefill kernels like any f16 view (their tiles reach LDS by
+            // direct global-to-LDS copies, which cannot convert)
+            const int64_t Bk = k->ne[3];
+            const int64_t per = Bk * Nkv * Hkv * D;
+            if ((size_t)(2 * per) * sizeof(_Float16) > kStageBytes) {
+                set_err(c, "F32 K/V staging needs %lld bytes; the context holds %zu",
+                        (long long)(2 * per * (int64_t)sizeof(_Float16)), kStageBytes);
+                return VXFA_NO_WORKSPACE;
+            }
+            _Float16* sk = c->stage;
+            _Float16* sv = c->stage + per;
+            e = vxfa::launch_to_f16(static_cast<const float*>(k->data), (int64_t)k->nb[1], (int64_t)k->nb[2],
+                                    (int64_t)k->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sk, st);
+            if (e == hipSuccess)
+                e = vxfa::launch_to_f16(static_cast<const float*>(v->data), (int64_t)v->nb[1], (int64_t)v->nb[2],
+                                        (int64_t)v->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sv, st);
+            if (e != hipSuccess) { set_err(c, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+            a.k = sk;
+            a.v = sv;
+            a.k_nb1 = a.v_nb1 = Hkv * D * 2;
+            a.k_nb2 = a.v_nb2 = D * 2;
+            a.k_nb3 = a.v_nb3 = Nkv * Hkv * D * 2;
+            a.kv_f32 = 0;
+        }
+        if (D == 64 && !mask && !implicit && !rope && scale != 0.0f && c->pp_enabled) {
+            // (scale 0 goes to the general kernel: the pipelined one folds the
+            // scale into the exponent and scores the partial block's dead rows -inf)
+            // encoder prefill: the software-pipelined hd 64 kernel
+            e = vxfa::launch_prefill64_pp(a, c->pp_shape, st);
+        } else {
+            // query-row wavefronts per workgroup (each with its KV partner
+            // wavefronts): 4 shares every staged K/V step among 128 query rows;
+            // hd 128 and small grids (fewer than 128 workgroups of 128 rows) use 2
+            const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
+            int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
+            if (c->waves_override == 2 || c->waves_override == 4) waves = c->waves_override;
+            e = vxfa::launch_prefill(a, (int)D, waves, st);
+        }
     }
     if (e != hipSuccess) {
         set_err(c, "kernel launch: %s", hipGetErrorString(e));
