@@ -73,8 +73,8 @@ typedef struct vxfa_tensor {
 
 /* Per-stream context (the analogue of a ggml backend context). Owns one
  * device workspace of fixed size, allocated by vxfa_ctx_create and freed by
- * vxfa_ctx_destroy: the split-KV arrival counters, the split-KV partial
- * records (partial O, running max and sum per split) and an f16 staging
+ * vxfa_ctx_destroy: the split-KV partial records (8 MiB: partial O,
+ * running max and sum per split) and an f16 staging
  * area for F32 K/V of prefill calls (32 MiB: K and V of up to 8192 rows of
  * 8 x 128). No other call allocates, frees or synchronises, so every call
  * can be captured into a HIP graph; a decode call whose batch would need more
@@ -85,8 +85,7 @@ typedef struct vxfa_tensor {
 typedef struct vxfa_ctx vxfa_ctx;
 
 /* Create a context bound to HIP device `device` and allocate its workspace
- * (about 50 MiB; the counters are zeroed and the device synchronised before
- * it returns). Returns NULL on failure. */
+ * (40 MiB). Returns NULL on failure. */
 vxfa_ctx* vxfa_ctx_create(int device);
 
 /* Destroy a context and free its workspace. NULL is accepted. */

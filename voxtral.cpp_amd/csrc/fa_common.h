@@ -26,7 +26,6 @@ struct AttnArgs {
     const uint16_t* mask; // F16 bits, may be null
     float* dst;           // [B][Nq][Hq][D]
     float* ws;            // split-KV partial records (decode)
-    uint32_t* cnt;        // split-KV arrival counters, one per (batch, kv head); zero between calls
     int64_t q_nb1, q_nb2, q_nb3;   // bytes
     int64_t k_nb1, k_nb2, k_nb3;   // bytes
     int64_t v_nb1, v_nb2, v_nb3;   // bytes
@@ -331,7 +330,7 @@ __device__ __forceinline__ float pair32_sum(float x) {
 // Host-side launchers (implemented in the kernel translation units).
 namespace vxfa {
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t stream);
-constexpr int kDecodeMaxSplit = 32;  // split workgroups per (batch, kv head)
+constexpr int kDecodeMaxSplit = 64;  // split workgroups per (batch, kv head)
 constexpr int kDecodeWaves = 4;      // wavefronts per decode workgroup
 // Floats per decode partial record: O [G][D], then m [G] and l [G], padded to
 // a multiple of 4 so every record starts 16-byte aligned.

@@ -9,21 +9,27 @@
 // src/voxtral.cpp:1126-1136); F32 tiles are rounded to f16 as they are
 // loaded for the QK^T product and used as F32 in the P.V product.
 //
-// Grid (n_split * Hkv, B), kDecodeWaves wavefronts per workgroup, the kv head
-// fastest-varying: neighbouring workgroups stream neighbouring head slices of
-// the same cache rows, and with 8 kv heads all splits of one head land on one
-// XCD (workgroups are dealt to the 8 XCDs round robin), so their partial
-// records stay in that XCD's L2. Each workgroup reduces one contiguous slice
-// of the live KV range to (O, m, l) per query head of its group.
-//
-// Merge of the splits, in the same launch: every workgroup stores its partial
-// record, makes it visible device-wide (release fence) and counts itself in
-// on its (batch, kv head) arrival counter; the workgroup that arrives last
-// (acquire fence) merges the n_split records in a fixed order — the output
-// does not depend on arrival order — writes the output and sets the counter
-// back to zero. Counters are zero when the context is created and every
-// launch leaves them at zero. With n_split == 1 the workgroup writes the
-// output directly.
+// Two kernels on the caller's stream:
+//   fa_decode         grid (n_split * Hkv, B), kDecodeWaves wavefronts per
+//                     workgroup, the kv head fastest-varying (neighbouring
+//                     workgroups stream neighbouring head slices of the same
+//                     cache rows). Each workgroup reduces one contiguous slice
+//                     of the live KV range to (O, m, l) per query head of its
+//                     group; with n_split == 1 it writes the output directly.
+//   fa_decode_combine grid (Hq * D / 32, B), one wavefront per (query head,
+//                     32 output dims): log-sum-exp merge of the n_split
+//                     partials in a fixed order (deterministic output); runs
+//                     only when n_split > 1.
+// The kernel boundary orders the partial records' stores before the merge's
+// loads. A merge inside the first kernel by the last workgroup of each
+// (batch, kv head) to finish — records written with device-scope stores, a
+// device-scope arrival counter, records read back with device-scope loads,
+// no cache maintenance — was built and measured slower at n_kv 8192 (split
+// work alone 11.4 us; waiting for the stores plus the counter +2.1 us; the
+// last workgroup's merge +3.9 us, one CU pulling every record through
+// device-scope round trips) than the kernel boundary plus a 128-workgroup
+// combine (about 3 us); with device-scope fences instead it was +13 us (each
+// fence writes back and invalidates the whole L2 of its XCD).
 //
 // Inside a wavefront (tiles of TP positions, 32 for f16 and 16 for F32 K/V,
 // so a tile is 16 KB either way; software pipelined: the next tile's K/V
@@ -56,84 +62,68 @@ namespace vxfa {
 constexpr int DEC_WAVES = kDecodeWaves;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 
-// Log-sum-exp merge of the n_split partial records of one (batch, kv head)
-// (its G query heads), run by the workgroup that arrived last:
+// Log-sum-exp merge of the n_split partial records, one wavefront per
+// (query head, 32 output dims):
 //   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
-// The O partials are loaded first (their addresses do not depend on the
-// weights; loads past the last split read the last record again, so all of
-// them issue back to back), then wavefront 0 loads the n_split (m, l) pairs,
-// one split per lane, and forms the weights with wavefront reductions: one
-// memory round trip. The summation order is fixed: the output is
-// deterministic.
+// Lane (f, grp) loads float4 f of the slice from splits grp, grp + 8, ...
+// while lane s loads split s's (m, l); all loads issue back to back (loads
+// past the last split read the last record again; their weights are zero), so
+// the merge costs one memory round trip. Wavefront reductions form the
+// weights and the sums, in a fixed order: the output is deterministic.
 template <int D, int G>
-__device__ __forceinline__ void merge_records(const AttnArgs& a, const float* base, int b, int g,
-                                              float (*cw)[kDecodeMaxSplit], float* cl, floatx4* cpart) {
-    constexpr int NF4 = G * D / 4;                              // float4 per record's O block
-    constexpr int NGRP = DEC_THREADS / NF4;                     // split groups
-    constexpr int MAXS = (kDecodeMaxSplit + NGRP - 1) / NGRP;   // splits per thread
+__global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
+    constexpr int CSUB = D / 32;                  // 32-dim slices per head
+    constexpr int CF4 = 8;                        // float4 per slice
+    constexpr int NGRP = 64 / CF4;                // split groups
+    constexpr int MAXS = kDecodeMaxSplit / NGRP;  // splits per lane
     constexpr int RS = dec_record_floats(D, G);
-    static_assert(NGRP * NF4 == DEC_THREADS, "merge split");
-    static_assert(kDecodeMaxSplit <= 64, "one (m, l) pair per lane of wavefront 0");
-    static_assert(RS % 4 == 0, "16-byte aligned records");
-    const int tid = threadIdx.x;
+    static_assert(kDecodeMaxSplit == 64, "one (m, l) pair per lane");
+    const int lane = threadIdx.x;
+    const int hq = blockIdx.x / CSUB, sl = blockIdx.x % CSUB;
+    const int g = hq / G, h = hq % G;
+    const int b = blockIdx.y;
     const int ns = a.n_split;
-    const int f = tid % NF4, grp = tid / NF4;
-    const int h = f / (D / 4);
+    const float* base = a.ws + (int64_t)(b * a.hkv + g) * ns * RS;
+    const int f = lane % CF4, grp = lane / CF4;
 
     floatx4 o[MAXS];
 #pragma unroll
     for (int i = 0; i < MAXS; ++i) {
         const int sp = min(grp + i * NGRP, ns - 1);
-        o[i] = *(const floatx4*)(base + (int64_t)sp * RS + 4 * f);
+        o[i] = *(const floatx4*)(base + (int64_t)sp * RS + h * D + 32 * sl + 4 * f);
     }
-    if (tid < 64) {
-        const float* r = base + (int64_t)min(tid, ns - 1) * RS + G * D;
-        float m[G], l[G];
+    const float* r = base + (int64_t)min(lane, ns - 1) * RS + G * D;
+    float m = r[h], l = r[G + h];
+    m = lane < ns ? m : -INFINITY;
+    l = lane < ns ? l : 0.f;
+    float M = m;
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            m[j] = r[j];
-            l[j] = r[G + j];
-        }
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    const float w = exp2_fast(m - Ms);            // 0 for an empty split (m = -inf)
+    float L = w * l;
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            m[j] = tid < ns ? m[j] : -INFINITY;
-            l[j] = tid < ns ? l[j] : 0.f;
-            float M = m[j];
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-            const float Ms = (M == -INFINITY) ? 0.f : M;
-            const float w = exp2_fast(m[j] - Ms);   // 0 for an empty split (m = -inf)
-            float L = w * l[j];
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
-            if (tid < kDecodeMaxSplit) cw[j][tid] = w;
-            if (tid == 0) cl[j] = L;
-        }
-    }
-    __syncthreads();
+    for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
+
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < MAXS; ++i) {
         const int sp = grp + i * NGRP;
-        const float w = sp < ns ? cw[h][sp] : 0.f;
-        acc[0] = fmaf(w, o[i][0], acc[0]);
-        acc[1] = fmaf(w, o[i][1], acc[1]);
-        acc[2] = fmaf(w, o[i][2], acc[2]);
-        acc[3] = fmaf(w, o[i][3], acc[3]);
+        const float ws = __shfl(w, sp & 63, 64);
+        const float wt = sp < ns ? ws : 0.f;
+        acc[0] = fmaf(wt, o[i][0], acc[0]);
+        acc[1] = fmaf(wt, o[i][1], acc[1]);
+        acc[2] = fmaf(wt, o[i][2], acc[2]);
+        acc[3] = fmaf(wt, o[i][3], acc[3]);
     }
-    cpart[grp * NF4 + f] = acc;
-    __syncthreads();
-    if (tid < NF4) {
-        floatx4 s = cpart[tid];
 #pragma unroll
-        for (int p = 1; p < NGRP; ++p) {
-            const floatx4 y = cpart[p * NF4 + tid];
-            s[0] += y[0]; s[1] += y[1]; s[2] += y[2]; s[3] += y[3];
-        }
-        const float L = cl[tid / (D / 4)];
+    for (int off = CF4; off < 64; off <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += shfl_xor(acc[c], off);
+    if (grp == 0) {
         const float inv = (L == 0.f) ? 0.f : 1.0f / L;
-        const floatx4 out = {s[0] * inv, s[1] * inv, s[2] * inv, s[3] * inv};
-        *(floatx4*)(a.dst + ((int64_t)b * a.hq + g * G) * D + 4 * tid) = out;
+        const floatx4 out = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        *(floatx4*)(a.dst + ((int64_t)b * a.hq + hq) * D + 32 * sl + 4 * f) = out;
     }
 }
 
@@ -156,10 +146,6 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     __shared__ int lds_red[2 * DEC_WAVES];
     __shared__ half8 lds_q[G * D / 8];   // the group's query heads, f16, [G][D]
     __shared__ float2 lds_rope[D / 2];   // cos / sin of each pair's rotary angle (with rope_pos)
-    __shared__ float lds_cw[G][kDecodeMaxSplit];
-    __shared__ float lds_cl[G];
-    __shared__ floatx4 lds_cpart[DEC_THREADS];
-    __shared__ int lds_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -168,7 +154,6 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     const int split = blockIdx.x / a.hkv;
     const int b = blockIdx.y;
     const int bkv = b / (a.b / a.bk);
-    const int pair = b * a.hkv + g;
     constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
     // rotary position of the query token (also the appended row's: the host
     // requires one kv batch per q batch), requested before any other load. A
@@ -535,8 +520,9 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     }
     __syncthreads();
 
-    constexpr int RS = dec_record_floats(D, G);
-    float* rec = a.n_split > 1 ? a.ws + ((int64_t)pair * a.n_split + split) * RS : nullptr;
+    float* rec = nullptr;
+    if (a.n_split > 1)
+        rec = a.ws + ((int64_t)(b * a.hkv + g) * a.n_split + split) * dec_record_floats(D, G);
     for (int o = tid; o < G * D; o += DEC_THREADS) {
         const int h = o / D, d = o % D;
         float M = lds_m[0][h];
@@ -557,20 +543,6 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
             if (d == 0) { rec[G * D + h] = M; rec[G * D + G + h] = L; }
         }
     }
-    if (rec == nullptr) return;
-
-    // ---- split merge by the last workgroup of this (batch, kv head) ---------
-    __threadfence();   // release: this workgroup's record before its count
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(a.cnt + pair, 1u);
-        lds_last = prev == (uint32_t)(a.n_split - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!lds_last) return;
-    __threadfence();   // acquire: every other record is visible
-    merge_records<D, G>(a, a.ws + (int64_t)pair * a.n_split * RS, b, g, lds_cw, lds_cl, lds_cpart);
-    if (tid == 0) atomicExch(a.cnt + pair, 0u);   // ready for the next call
 }
 
 template <int D, int G, bool KV32>
@@ -583,6 +555,8 @@ static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
         if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32>), grid, block, 0, st, a);
     }
+    if (a.n_split > 1)
+        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G * (D / 32), a.b), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -593,7 +567,7 @@ static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
 
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t st) {
     if (a.n_split < 1 || a.n_split > kDecodeMaxSplit) return hipErrorInvalidValue;
-    if (a.n_split > 1 && (a.ws == nullptr || a.cnt == nullptr)) return hipErrorInvalidValue;
+    if (a.n_split > 1 && a.ws == nullptr) return hipErrorInvalidValue;
     if (a.b > 65535 || (int64_t)a.n_split * a.hkv > 0x7fffffff) return hipErrorInvalidValue;
     if (a.kv_f32 && a.append) return hipErrorInvalidValue;
     if (head_dim == 128) {

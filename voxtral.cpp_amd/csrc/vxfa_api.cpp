@@ -20,17 +20,14 @@
 #include "fa_common.h"
 
 // Device workspace of a context, allocated once by vxfa_ctx_create (no call
-// allocates, frees or synchronises): the split-KV arrival counters (zeroed at
-// creation; every launch leaves them at zero), the split-KV partial records,
-// and f16 staging for F32 K/V of prefill calls.
-constexpr size_t kCounterSlots = 65536;                 // (batch, kv head) pairs with a split merge
-constexpr size_t kRecordBytes = (size_t)18 << 20;       // 256 pairs x 32 splits of G = 4, hd 128
+// allocates, frees or synchronises): the split-KV partial records and f16
+// staging for F32 K/V of prefill calls.
+constexpr size_t kRecordBytes = (size_t)8 << 20;        // e.g. 256 (batch, kv head) pairs x 8 splits, or 8 x 64
 constexpr size_t kStageBytes = (size_t)32 << 20;        // F32 K and V of 8192 rows x 1024 as f16
 
 struct vxfa_ctx {
     int device = 0;
-    char* ws = nullptr;           // one device allocation holding the three regions
-    uint32_t* cnt = nullptr;      // kCounterSlots arrival counters
+    char* ws = nullptr;           // one device allocation holding both regions
     float* rec = nullptr;         // kRecordBytes of partial records
     _Float16* stage = nullptr;    // kStageBytes of f16 K/V staging
     char last_error[256] = {0};
@@ -212,10 +209,9 @@ int choose_split(int64_t pairs, int64_t nkv) {
 }
 
 // The split count the context's workspace can hold: pairs * S records of
-// rec_floats each, and one arrival counter per pair (else no split).
+// rec_floats each (else fewer splits, down to none).
 int fit_split(int S, int64_t pairs, int rec_floats) {
     if (S <= 1) return 1;
-    if (pairs > (int64_t)kCounterSlots) return 1;
     const int64_t cap = (int64_t)(kRecordBytes / sizeof(float)) / (pairs * rec_floats);
     if (cap < 2) return 1;
     return S < cap ? S : (int)cap;
@@ -237,21 +233,14 @@ vxfa_ctx* vxfa_ctx_create(int device) {
     if (const char* e = getenv("VXFA_PP_SHAPE")) c->pp_shape = atoi(e);
     int prev = 0;
     (void)hipGetDevice(&prev);
-    const size_t cnt_bytes = kCounterSlots * sizeof(uint32_t);
-    const size_t total = cnt_bytes + kRecordBytes + kStageBytes;
-    bool ok = hipSetDevice(device) == hipSuccess && hipMalloc(&c->ws, total) == hipSuccess;
-    // the counters start at zero; the synchronisation makes that so before any
-    // call (a call may be captured into a graph, so it must not clear them)
-    ok = ok && hipMemset(c->ws, 0, cnt_bytes) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+    const bool ok = hipSetDevice(device) == hipSuccess && hipMalloc(&c->ws, kRecordBytes + kStageBytes) == hipSuccess;
     (void)hipSetDevice(prev);
     if (!ok) {
-        if (c->ws) (void)hipFree(c->ws);
         delete c;
         return nullptr;
     }
-    c->cnt = reinterpret_cast<uint32_t*>(c->ws);
-    c->rec = reinterpret_cast<float*>(c->ws + cnt_bytes);
-    c->stage = reinterpret_cast<_Float16*>(c->ws + cnt_bytes + kRecordBytes);
+    c->rec = reinterpret_cast<float*>(c->ws);
+    c->stage = reinterpret_cast<_Float16*>(c->ws + kRecordBytes);
     return c;
 }
 
@@ -443,7 +432,6 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
         S = fit_split(S, B * Hkv, vxfa::dec_record_floats((int)D, (int)G));
         a.n_split = S;
         a.ws = c->rec;
-        a.cnt = c->cnt;
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
         if (a.kv_f32) {
