@@ -25,20 +25,48 @@
 constexpr size_t kRecordBytes = (size_t)8 << 20;        // e.g. 256 (batch, kv head) pairs x 8 splits, or 8 x 64
 constexpr size_t kStageBytes = (size_t)32 << 20;        // F32 K and V of 8192 rows x 1024 as f16
 
-struct vxfa_ctx {
-    int device = 0;
-    char* ws = nullptr;           // one device allocation holding both regions
-    float* rec = nullptr;         // kRecordBytes of partial records
-    _Float16* stage = nullptr;    // kStageBytes of f16 K/V staging
-    char last_error[256] = {0};
-    // launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
-    // VXFA_PREFILL_WAVES), read once when the context is created; 0 = heuristic
+// Launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
+// VXFA_PREFILL_WAVES, VXFA_PREFILL_PP, VXFA_PP_SHAPE), read from the
+// environment; 0 = heuristic.
+struct Tuning {
     int split_override = 0;
     int waves_override = 0;
     // VXFA_PREFILL_PP=0 routes hd 64 unmasked prefill to the general kernel;
     // VXFA_PP_SHAPE picks its workgroup shape (1 or 2, 0 = default)
     bool pp_enabled = true;
     int pp_shape = 0;
+    void read_env() {
+        if (const char* e = getenv("VXFA_DECODE_SPLIT")) split_override = atoi(e);
+        if (const char* e = getenv("VXFA_PREFILL_WAVES")) waves_override = atoi(e);
+        if (const char* e = getenv("VXFA_PREFILL_PP")) pp_enabled = atoi(e) != 0;
+        if (const char* e = getenv("VXFA_PP_SHAPE")) pp_shape = atoi(e);
+    }
+};
+
+// Where one call may put its device scratch (split-KV partial records of a
+// decode call, f16 staging of F32 K/V of a prefill call) and its error
+// message: a context's workspace, or the library's static scratch array.
+struct Workspace {
+    int device;
+    float* rec;           // split-KV partial records
+    size_t rec_bytes;
+    _Float16* stage;      // f16 staging of F32 K/V (prefill)
+    size_t stage_bytes;
+    char* err;            // message of the last failure
+    size_t err_len;
+    Tuning tune;
+};
+
+struct vxfa_ctx {
+    int device = 0;
+    char* ws = nullptr;           // one device allocation holding both regions
+    float* rec = nullptr;         // kRecordBytes of partial records
+    _Float16* stage = nullptr;    // kStageBytes of f16 K/V staging
+    char last_error[256] = {0};
+    Tuning tune;                  // read once when the context is created
+    Workspace view() {
+        return Workspace{device, rec, kRecordBytes, stage, kStageBytes, last_error, sizeof(last_error), tune};
+    }
 };
 
 namespace {
@@ -46,11 +74,10 @@ namespace {
 constexpr int kVersion = 1 * 10000 + 1 * 100 + 0;
 constexpr int kMaskedSplitCap = 32;
 
-void set_err(vxfa_ctx* c, const char* fmt, ...) {
-    if (!c) return;
+void set_err(Workspace& w, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(c->last_error, sizeof(c->last_error), fmt, ap);
+    vsnprintf(w.err, w.err_len, fmt, ap);
     va_end(ap);
 }
 
@@ -208,11 +235,11 @@ int choose_split(int64_t pairs, int64_t nkv) {
     return (int)s;
 }
 
-// The split count the context's workspace can hold: pairs * S records of
+// The split count a workspace of rec_bytes can hold: pairs * S records of
 // rec_floats each (else fewer splits, down to none).
-int fit_split(int S, int64_t pairs, int rec_floats) {
+int fit_split(int S, int64_t pairs, int rec_floats, size_t rec_bytes) {
     if (S <= 1) return 1;
-    const int64_t cap = (int64_t)(kRecordBytes / sizeof(float)) / (pairs * rec_floats);
+    const int64_t cap = (int64_t)(rec_bytes / sizeof(float)) / (pairs * rec_floats);
     if (cap < 2) return 1;
     return S < cap ? S : (int)cap;
 }
@@ -227,10 +254,7 @@ vxfa_ctx* vxfa_ctx_create(int device) {
     vxfa_ctx* c = new (std::nothrow) vxfa_ctx();
     if (!c) return nullptr;
     c->device = device;
-    if (const char* e = getenv("VXFA_DECODE_SPLIT")) c->split_override = atoi(e);
-    if (const char* e = getenv("VXFA_PREFILL_WAVES")) c->waves_override = atoi(e);
-    if (const char* e = getenv("VXFA_PREFILL_PP")) c->pp_enabled = atoi(e) != 0;
-    if (const char* e = getenv("VXFA_PP_SHAPE")) c->pp_shape = atoi(e);
+    c->tune.read_env();
     int prev = 0;
     (void)hipGetDevice(&prev);
     const bool ok = hipSetDevice(device) == hipSuccess && hipMalloc(&c->ws, kRecordBytes + kStageBytes) == hipSuccess;
@@ -285,12 +309,11 @@ namespace {
 // The op, with either a mask tensor (`mask`), an implicit causal / window mask
 // (`im`, kind VXFA_MASK_CAUSAL) or neither; never both (the entry points
 // enforce it).
-int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
+int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v, const vxfa_tensor* mask,
         const vxfa_mask_desc* im, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream,
         const vxfa_tensor* k_new = nullptr, const vxfa_tensor* v_new = nullptr, const vxfa_ring* ring = nullptr,
         const vxfa_rope* rope = nullptr) {
-    if (!c) return VXFA_INVALID_ARG;
-    c->last_error[0] = 0;
+    w.err[0] = 0;
     const char* why = nullptr;
     int rc = check(q, k, v, mask, dst, scale, max_bias, logit_softcap, &why);
     if (rc == VXFA_OK && k_new) rc = check_append(k, v, k_new, v_new, &why);
@@ -327,7 +350,7 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
         }
     }
     if (rc != VXFA_OK) {
-        set_err(c, "%s", why);
+        set_err(w, "%s", why);
         return rc;
     }
     const bool append = k_new != nullptr && k_new->ne[1] > 0;
@@ -339,8 +362,8 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
     const bool fuse_append = append && Nq == 1 && k_new->ne[1] == 1 && (Gq == 1 || Gq == 2 || Gq == 4) &&
                              Nq * Hq * B > 0;
 
-    hipError_t e = hipSetDevice(c->device);
-    if (e != hipSuccess) { set_err(c, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    hipError_t e = hipSetDevice(w.device);
+    if (e != hipSuccess) { set_err(w, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     // rotary embedding: ggml's theta scale, computed as ggml_rope_ext's CPU path does
     const float rope_ts = rope ? powf(rope->freq_base, -2.0f / (float)rope->n_dims) : 0.0f;
@@ -352,13 +375,13 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
             ap.rope_dims = rope->n_dims;
         }
         e = vxfa::launch_kv_append(ap, st);
-        if (e != hipSuccess) { set_err(c, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+        if (e != hipSuccess) { set_err(w, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     }
     if (Nq * Hq * B == 0) return VXFA_OK;
 
     if (Nkv == 0) {
         e = vxfa::launch_zero(static_cast<float*>(dst->data), Nq * Hq * B * D, st);
-        if (e != hipSuccess) { set_err(c, "zero fill: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+        if (e != hipSuccess) { set_err(w, "zero fill: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
         return VXFA_OK;
     }
 
@@ -427,11 +450,11 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
             if (s2 > S) S = (int)(s2 < (Nkv + 63) / 64 ? s2 : (Nkv + 63) / 64);
         }
         if (mask && S > kMaskedSplitCap) S = kMaskedSplitCap;
-        if (c->split_override > 0) S = c->split_override;
+        if (w.tune.split_override > 0) S = w.tune.split_override;
         if (S > vxfa::kDecodeMaxSplit) S = vxfa::kDecodeMaxSplit;
-        S = fit_split(S, B * Hkv, vxfa::dec_record_floats((int)D, (int)G));
+        S = fit_split(S, B * Hkv, vxfa::dec_record_floats((int)D, (int)G), w.rec_bytes);
         a.n_split = S;
-        a.ws = c->rec;
+        a.ws = w.rec;
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
         if (a.kv_f32) {
@@ -441,19 +464,19 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
             // direct global-to-LDS copies, which cannot convert)
             const int64_t Bk = k->ne[3];
             const int64_t per = Bk * Nkv * Hkv * D;
-            if ((size_t)(2 * per) * sizeof(_Float16) > kStageBytes) {
-                set_err(c, "F32 K/V staging needs %lld bytes; the context holds %zu",
-                        (long long)(2 * per * (int64_t)sizeof(_Float16)), kStageBytes);
+            if ((size_t)(2 * per) * sizeof(_Float16) > w.stage_bytes) {
+                set_err(w, "F32 K/V staging needs %lld bytes; the workspace holds %zu",
+                        (long long)(2 * per * (int64_t)sizeof(_Float16)), w.stage_bytes);
                 return VXFA_NO_WORKSPACE;
             }
-            _Float16* sk = c->stage;
-            _Float16* sv = c->stage + per;
+            _Float16* sk = w.stage;
+            _Float16* sv = w.stage + per;
             e = vxfa::launch_to_f16(static_cast<const float*>(k->data), (int64_t)k->nb[1], (int64_t)k->nb[2],
                                     (int64_t)k->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sk, st);
             if (e == hipSuccess)
                 e = vxfa::launch_to_f16(static_cast<const float*>(v->data), (int64_t)v->nb[1], (int64_t)v->nb[2],
                                         (int64_t)v->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sv, st);
-            if (e != hipSuccess) { set_err(c, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+            if (e != hipSuccess) { set_err(w, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
             a.k = sk;
             a.v = sv;
             a.k_nb1 = a.v_nb1 = Hkv * D * 2;
@@ -461,23 +484,23 @@ int run(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tens
             a.k_nb3 = a.v_nb3 = Nkv * Hkv * D * 2;
             a.kv_f32 = 0;
         }
-        if (D == 64 && !mask && !implicit && !rope && scale != 0.0f && c->pp_enabled) {
+        if (D == 64 && !mask && !implicit && !rope && scale != 0.0f && w.tune.pp_enabled) {
             // (scale 0 goes to the general kernel: the pipelined one folds the
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel
-            e = vxfa::launch_prefill64_pp(a, c->pp_shape, st);
+            e = vxfa::launch_prefill64_pp(a, w.tune.pp_shape, st);
         } else {
             // query-row wavefronts per workgroup (each with its KV partner
             // wavefronts): 4 shares every staged K/V step among 128 query rows;
             // hd 128 and small grids (fewer than 128 workgroups of 128 rows) use 2
             const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
             int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
-            if (c->waves_override == 2 || c->waves_override == 4) waves = c->waves_override;
+            if (w.tune.waves_override == 2 || w.tune.waves_override == 4) waves = w.tune.waves_override;
             e = vxfa::launch_prefill(a, (int)D, waves, st);
         }
     }
     if (e != hipSuccess) {
-        set_err(c, "kernel launch: %s", hipGetErrorString(e));
+        set_err(w, "kernel launch: %s", hipGetErrorString(e));
         return VXFA_HIP_ERROR;
     }
     return VXFA_OK;
@@ -490,24 +513,27 @@ extern "C" {
 int vxfa_flash_attn_ext(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v,
                         const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias, float logit_softcap,
                         void* stream) {
-    return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream);
+    if (!c) return VXFA_INVALID_ARG;
+    Workspace w = c->view();
+    return run(w, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream);
 }
 
 int vxfa_kv_append(vxfa_ctx* c, const vxfa_tensor* k_new, const vxfa_tensor* v_new, vxfa_tensor* k, vxfa_tensor* v,
                    void* stream) {
     if (!c) return VXFA_INVALID_ARG;
     c->last_error[0] = 0;
-    if (!k || !v) { set_err(c, "k and v are required"); return VXFA_INVALID_ARG; }
+    Workspace w = c->view();
+    if (!k || !v) { set_err(w, "k and v are required"); return VXFA_INVALID_ARG; }
     const char* why = nullptr;
     const int rc = check_append(k, v, k_new, v_new, &why);
     if (rc != VXFA_OK) {
-        set_err(c, "%s", why);
+        set_err(w, "%s", why);
         return rc;
     }
     hipError_t e = hipSetDevice(c->device);
-    if (e != hipSuccess) { set_err(c, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    if (e != hipSuccess) { set_err(w, "hipSetDevice: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     e = vxfa::launch_kv_append(append_args(k, v, k_new, v_new), reinterpret_cast<hipStream_t>(stream));
-    if (e != hipSuccess) { set_err(c, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+    if (e != hipSuccess) { set_err(w, "kv append: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
     return VXFA_OK;
 }
 
@@ -515,24 +541,24 @@ int vxfa_flash_attn_ext_append(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k
                                const vxfa_tensor* k_new, const vxfa_tensor* v_new, const vxfa_tensor* mask,
                                vxfa_tensor* dst, float scale, float max_bias, float logit_softcap, void* stream) {
     if (!c) return VXFA_INVALID_ARG;
+    Workspace w = c->view();
     if (!k_new || !v_new) {
-        c->last_error[0] = 0;
-        set_err(c, "k_new and v_new are required");
+        set_err(w, "k_new and v_new are required");
         return VXFA_INVALID_ARG;
     }
-    return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new);
+    return run(w, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new);
 }
 
 int vxfa_flash_attn_ext_ring(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, vxfa_tensor* v, const vxfa_ring* ring,
                              const vxfa_tensor* k_new, const vxfa_tensor* v_new, vxfa_tensor* dst, float scale,
                              float max_bias, float logit_softcap, void* stream) {
     if (!c) return VXFA_INVALID_ARG;
+    Workspace w = c->view();
     if (!ring || (k_new == nullptr) != (v_new == nullptr)) {
-        c->last_error[0] = 0;
-        set_err(c, "a ring descriptor is required; k_new and v_new come together");
+        set_err(w, "a ring descriptor is required; k_new and v_new come together");
         return VXFA_INVALID_ARG;
     }
-    return run(c, q, k, v, nullptr, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, ring);
+    return run(w, q, k, v, nullptr, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, ring);
 }
 
 int vxfa_flash_attn_ext_rope(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, vxfa_tensor* v,
@@ -540,12 +566,12 @@ int vxfa_flash_attn_ext_rope(vxfa_ctx* c, const vxfa_tensor* q, vxfa_tensor* k, 
                              const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias,
                              float logit_softcap, void* stream) {
     if (!c) return VXFA_INVALID_ARG;
+    Workspace w = c->view();
     if (!rope || !k_new || !v_new) {
-        c->last_error[0] = 0;
-        set_err(c, "rope, k_new and v_new are required");
+        set_err(w, "rope, k_new and v_new are required");
         return VXFA_INVALID_ARG;
     }
-    return run(c, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, nullptr, rope);
+    return run(w, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream, k_new, v_new, nullptr, rope);
 }
 
 int vxfa_check_mask_desc(const vxfa_mask_desc* m) {
@@ -559,11 +585,12 @@ int vxfa_flash_attn_ext_implicit(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_t
                                  const vxfa_mask_desc* mask, vxfa_tensor* dst, float scale, float max_bias,
                                  float logit_softcap, void* stream) {
     if (!c) return VXFA_INVALID_ARG;
+    Workspace w = c->view();
     if (vxfa_check_mask_desc(mask) != VXFA_OK) {
-        set_err(c, "mask descriptor: kind must be VXFA_MASK_NONE or VXFA_MASK_CAUSAL and window >= 0");
+        set_err(w, "mask descriptor: kind must be VXFA_MASK_NONE or VXFA_MASK_CAUSAL and window >= 0");
         return VXFA_INVALID_ARG;
     }
-    return run(c, q, k, v, nullptr, mask, dst, scale, max_bias, logit_softcap, stream);
+    return run(w, q, k, v, nullptr, mask, dst, scale, max_bias, logit_softcap, stream);
 }
 
 }  // extern "C"
