@@ -252,10 +252,30 @@ int vxfa_flash_attn_ext_rope(vxfa_ctx* ctx, const vxfa_tensor* q,
                              float scale, float max_bias, float logit_softcap,
                              void* stream);
 
+/* GGML_OP_FLASH_ATTN_EXT without a context and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory or create a context at that point (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * contract, results and status codes as vxfa_flash_attn_ext, on the current
+ * HIP device and `stream`; the scratch it needs (split-KV partial records of
+ * a decode step, f16 staging of F32 K/V for a prefill call) lives in a
+ * static 8 MiB array in the library's code object, one per GPU, kept until
+ * the process ends. Limits: F32 K/V prefill calls whose f16 K and V exceed
+ * 8 MiB return VXFA_NO_WORKSPACE; decode steps always run (with fewer
+ * splits if their records would not fit, which the call shapes of voxtral
+ * never reach). Every call on one GPU shares the array, so calls that
+ * overlap on one GPU race. Its messages are read with vxfa_last_error(NULL)
+ * (per calling thread). */
+int vxfa_flash_attn_ext_noalloc(const vxfa_tensor* q, const vxfa_tensor* k,
+                                const vxfa_tensor* v, const vxfa_tensor* mask,
+                                vxfa_tensor* dst, float scale, float max_bias,
+                                float logit_softcap, void* stream);
+
 /* Human-readable name of a status code (static storage). */
 const char* vxfa_status_str(int status);
 
-/* Message for the last failing call on this context ("" if none). */
+/* Message for the last failing call on this context ("" if none); with
+ * NULL, for the calling thread's last vxfa_flash_attn_ext_noalloc call. */
 const char* vxfa_last_error(const vxfa_ctx* ctx);
 
 /* Library version: major * 10000 + minor * 100 + patch. */

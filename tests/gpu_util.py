@@ -107,6 +107,17 @@ class Runner:
         out = self._finish(case, buf, dev, self._inputs(case) if verify_inputs else ())
         return rc, out
 
+    def run_noalloc(self, case, dev=None, check=True):
+        """The case through vxfa_flash_attn_ext_noalloc (no context; the
+        library's static scratch) on the current device and stream."""
+        dev = dev if dev is not None else to_device(case)
+        d = descs(case, dev)
+        buf, dst = self._dst(case)
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = vxfa.flash_attn_ext_noalloc(d["q"], d["k"], d["v"], d.get("mask"), dst, case.scale, stream=stream,
+                                         check=check)
+        return rc, self._finish(case, buf, dev, self._inputs(case))
+
     def run_implicit(self, case, mask_desc, dev=None, check=True):
         """The case's q/k/v through vxfa_flash_attn_ext_implicit (its mask
         tensor, if any, is not passed)."""

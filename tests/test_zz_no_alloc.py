@@ -1,0 +1,67 @@
+"""vxfa_flash_attn_ext_noalloc: the op with no context and no allocation,
+its scratch in the library's static per-GPU array. Each call is checked
+against vxfa_flash_attn_ext on the same device bytes (same kernels, same
+split choice: identical bits) and, for the decode steps, against the oracle
+at the parity bar; calls come in a row with the later ones smaller, so the
+array keeps an earlier call's contents."""
+import numpy as np
+import pytest
+
+import cases
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+@pytest.fixture(scope="module")
+def runner():
+    import gpu_util
+    r = gpu_util.Runner()
+    yield r
+    r.close()
+
+
+def _same(runner, c, oracle=False):
+    import gpu_util
+    dev = gpu_util.to_device(c)
+    rc, ref = runner.run(c, dev=dev)
+    assert rc == 0
+    rc, out = runner.run_noalloc(c, dev=dev)
+    assert rc == 0
+    print(f"[noalloc] {c.name}: max |noalloc - ctx| = {float(np.abs(out - ref).max()):.3e}", flush=True)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    if oracle:
+        m, r, ok = gpu_util.parity(out, cases.oracle_f64(c), ATOL, RTOL)
+        assert ok, (m, r)
+
+
+def test_noalloc_decode_then_smaller_decode(runner):
+    """n_kv 8192 (64 split records in the scratch), then n_kv 1000 (16)."""
+    _same(runner, cases.decode_case(8192, seed=301), oracle=True)
+    _same(runner, cases.decode_case(1000, seed=302), oracle=True)
+
+
+def test_noalloc_batched_then_single(runner):
+    _same(runner, cases.batched_case(16, capacity=2048, lo=100, hi=2048, seed=303))
+    _same(runner, cases.decode_case(333, hq=16, hkv=8, hd=64, seed=304))
+
+
+def test_noalloc_prefill_and_f32_staging(runner):
+    """Causal prefill (no scratch), F32 encoder K/V (7.7 MB of f16 staging in
+    the scratch), then a smaller F32 prefill."""
+    _same(runner, cases.prefill_case(439, seed=305))
+    _same(runner, cases.encoder_case(1500, 20, 64, seed=306, kv_f32=True))
+    _same(runner, cases.prefill_case(100, seed=307, kv_f32=True))
+
+
+def test_noalloc_rejects_staging_beyond_the_scratch(runner):
+    """F32 K and V of 16384 rows x 8 x 128 need 64 MiB of f16 staging: beyond
+    the 8 MiB scratch, the call returns VXFA_NO_WORKSPACE and launches nothing."""
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.prefill_case(2, seed=308, causal=False, kv_offset=16382, kv_f32=True)
+    rc, _ = runner.run_noalloc(c, check=False)
+    assert rc == vx.NO_WORKSPACE
+    msg = vx.load().vxfa_last_error(None).decode()
+    assert "staging" in msg, msg

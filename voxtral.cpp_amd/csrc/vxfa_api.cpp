@@ -14,6 +14,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 
 #include "../../include/vxfa.h"
@@ -68,6 +69,21 @@ struct vxfa_ctx {
         return Workspace{device, rec, kRecordBytes, stage, kStageBytes, last_error, sizeof(last_error), tune};
     }
 };
+
+// Device scratch of vxfa_flash_attn_ext_noalloc: a file-scope array in the
+// library's code object (each GPU holds its own copy until the process
+// ends), used for the same purposes as a context's workspace. Its device
+// address is looked up once per device (hipGetSymbolAddress) and kept; host
+// code uses only that address, never the array's name, which on the host is
+// a stand-in symbol, not device memory. Every call on one GPU shares the
+// array: calls that overlap on one GPU (two streams, two threads) race.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {nullptr};
+static thread_local char t_noalloc_err[256] = {0};   // message of this thread's last failing no-alloc call
 
 namespace {
 
@@ -298,7 +314,7 @@ const char* vxfa_status_str(int s) {
     }
 }
 
-const char* vxfa_last_error(const vxfa_ctx* c) { return c ? c->last_error : ""; }
+const char* vxfa_last_error(const vxfa_ctx* c) { return c ? c->last_error : t_noalloc_err; }
 
 int vxfa_version(void) { return kVersion; }
 
@@ -591,6 +607,45 @@ int vxfa_flash_attn_ext_implicit(vxfa_ctx* c, const vxfa_tensor* q, const vxfa_t
         return VXFA_INVALID_ARG;
     }
     return run(w, q, k, v, nullptr, mask, dst, scale, max_bias, logit_softcap, stream);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int vxfa_flash_attn_ext_noalloc(const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_tensor* v,
+                                const vxfa_tensor* mask, vxfa_tensor* dst, float scale, float max_bias,
+                                float logit_softcap, void* stream) {
+    t_noalloc_err[0] = 0;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess || device < 0 || device >= kMaxDevices) {
+        snprintf(t_noalloc_err, sizeof(t_noalloc_err), "no usable current HIP device");
+        return VXFA_HIP_ERROR;
+    }
+    void* ptr = nullptr;
+    {
+        // first call on this device (the device is current): the array's
+        // device address, once
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_ptr[device]) {
+            e = hipGetSymbolAddress(&g_scratch_ptr[device], HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !g_scratch_ptr[device]) {
+                g_scratch_ptr[device] = nullptr;
+                snprintf(t_noalloc_err, sizeof(t_noalloc_err), "hipGetSymbolAddress(scratch): %s",
+                         hipGetErrorString(e));
+                return VXFA_HIP_ERROR;
+            }
+        }
+        ptr = g_scratch_ptr[device];
+    }
+    Tuning tune;
+    tune.read_env();
+    // records (decode) and staging (prefill with F32 K/V) are never needed
+    // by one call together: both use the whole array
+    Workspace w{device, static_cast<float*>(ptr), kScratchBytes, static_cast<_Float16*>(ptr), kScratchBytes,
+                t_noalloc_err, sizeof(t_noalloc_err), tune};
+    return run(w, q, k, v, mask, nullptr, dst, scale, max_bias, logit_softcap, stream);
 }
 
 }  // extern "C"

@@ -31,6 +31,7 @@ EXPORTS = (
     "vxfa_flash_attn_ext_append",
     "vxfa_flash_attn_ext_ring",
     "vxfa_flash_attn_ext_rope",
+    "vxfa_flash_attn_ext_noalloc",
     "vxfa_status_str",
     "vxfa_last_error",
     "vxfa_version",
@@ -139,6 +140,9 @@ def load() -> ctypes.CDLL:
     L.vxfa_flash_attn_ext_rope.argtypes = [ctypes.c_void_p, P, P, P, P, P, ctypes.POINTER(VxfaRope), P, P,
                                            ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
     L.vxfa_flash_attn_ext_rope.restype = ctypes.c_int
+    L.vxfa_flash_attn_ext_noalloc.argtypes = [P, P, P, P, P, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                              ctypes.c_void_p]
+    L.vxfa_flash_attn_ext_noalloc.restype = ctypes.c_int
     L.vxfa_status_str.argtypes = [ctypes.c_int]
     L.vxfa_status_str.restype = ctypes.c_char_p
     L.vxfa_last_error.argtypes = [ctypes.c_void_p]
@@ -174,6 +178,19 @@ def _ref(t):
 def check_mask_desc(m) -> int:
     """Host-only validation of a mask descriptor (VxfaMaskDesc or None)."""
     return load().vxfa_check_mask_desc(_ref(m))
+
+
+def flash_attn_ext_noalloc(q, k, v, mask, dst, scale: float, max_bias: float = 0.0, logit_softcap: float = 0.0,
+                           stream: int = 0, check: bool = True) -> int:
+    """vxfa_flash_attn_ext_noalloc: the op on the current device without a
+    context; scratch in the library's static per-GPU array (calls that
+    overlap on one GPU race)."""
+    L = load()
+    rc = L.vxfa_flash_attn_ext_noalloc(_ref(q), _ref(k), _ref(v), _ref(mask), _ref(dst), scale, max_bias,
+                                       logit_softcap, ctypes.c_void_p(stream))
+    if check and rc != OK:
+        raise VxfaError(rc, L.vxfa_last_error(None).decode())
+    return rc
 
 
 def supports(q, k, v, mask, dst, scale: float, max_bias: float = 0.0, logit_softcap: float = 0.0) -> int:
