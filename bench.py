@@ -12,8 +12,10 @@ sliding-window decode and the 32-stream ragged batch. HBM-bound shapes rotate
 over per-layer buffers larger than the 256 MB MALL, so their bytes come from
 HBM; the sliding window is also reported warm (one cache).
 
-The CPU baseline is the ggml-faithful C restatement of the op (the oracle),
-timed on the host cores with min(hw threads, 16) threads, voxtral's default.
+The CPU baseline is ggml's one-row algorithm with its AVX2/F16C vector
+kernels (oracle/fa_cpu_simd.c, bit-identical to the scalar oracle in
+f16-accumulator mode), timed on every configuration at min(hw threads, 16)
+threads, voxtral's default, and at every hardware thread.
 """
 from __future__ import annotations
 
@@ -212,33 +214,159 @@ def decode_bytes(n_live, hq=32, hkv=8, hd=128, mask_bytes=0, elt=2):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline (the oracle), bounded sample
+# CPU baseline: ggml's one-row flash_attn_ext with its AVX2/F16C vector
+# kernels (oracle/fa_cpu_simd.c), bounded samples of every configuration, at
+# voxtral's default thread count min(hw, 16) and at every hardware thread
 
-def cpu_baseline_encoder(seq=1500, heads=20, hd=64, layers=5):
-    """`layers` encoder layers (about 10 s on 16 host cores) through the
-    ggml-faithful CPU restatement, each on its own seeded inputs."""
+def _cpu_inputs(kind, seed):
+    """Host tensors (oracle Views) of one call of configuration `kind`."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle
-    threads = oracle.default_threads()
-    views_ = []
-    for i in range(layers):
-        rng = np.random.default_rng(7 + i)
+    rng = np.random.default_rng(seed)
+    f16 = lambda shape, sigma=1.0: (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(
+        np.float16).view(np.uint16)
+    V = oracle.View
+    if kind == "encoder":
+        seq, heads, hd = 1500, 20, 64
         q = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).astype(np.float32)
-        k = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
-        v = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).view(np.uint16)
-        views_.append((oracle.View(q, oracle.F32, *views.encoder_qkv(seq, heads, hd, 4)),
-                       oracle.View(k, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)),
-                       oracle.View(v, oracle.F16, *views.encoder_qkv(seq, heads, hd, 2))))
-    t0 = time.perf_counter()
-    for qv, kv, vv in views_:
-        oracle.fa_ggml(qv, kv, vv, None, 0.125, vkq_f16=True, threads=threads)
-    dt = time.perf_counter() - t0
-    flops = 4.0 * seq * seq * hd * heads * layers
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{layers} encoder layers (1500x1500, 20 heads, hd64, distinct seeded inputs) through "
-                      f"oracle/fa_oracle.c (ggml one-row algorithm, f16 V accumulation), {dt:.2f} s",
-            "us_per_layer": dt / layers * 1e6}
+        return (V(q, oracle.F32, *views.encoder_qkv(seq, heads, hd, 4)),
+                V(f16((seq, heads, hd)), oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)),
+                V(f16((seq, heads, hd)), oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)), None, 0.125)
+    scale = f32s(1 / math.sqrt(128))
+    if kind in ("decode1024", "decode8192"):
+        n_kv = 1024 if kind == "decode1024" else 8192
+        kne, knb = views.kv_cache(n_kv, 8, 128, n_kv)
+        return (V(rng.standard_normal((1, 32, 128), dtype=np.float32), oracle.F32, *views.decoder_q(1, 32, 128)),
+                V(f16((n_kv, 8, 128)), oracle.F16, kne, knb), V(f16((n_kv, 8, 128)), oracle.F16, kne, knb), None, scale)
+    if kind == "prefill439":
+        n = 439
+        kne, knb = views.kv_cache(n, 8, 128, n)
+        mask = np.where(np.arange(n)[None, :] <= np.arange(n)[:, None], 0, 0xFC00).astype(np.uint16)
+        return (V(rng.standard_normal((n, 32, 128), dtype=np.float32), oracle.F32, *views.decoder_q(n, 32, 128)),
+                V(f16((n, 8, 128)), oracle.F16, kne, knb), V(f16((n, 8, 128)), oracle.F16, kne, knb),
+                V(mask, oracle.F16, *views.mask(n, n)), scale)
+    if kind == "sliding":
+        # one step of the streaming decode: cache of 16384 rows, n_kv 16335
+        # (the middle of the 100 steps), 2048-row window in the mask
+        cap, n_kv, window = 16384, 16335, 2048
+        kne, knb = views.kv_cache(n_kv, 8, 128, cap)
+        mask = np.zeros(n_kv, dtype=np.uint16)
+        mask[: n_kv - window] = 0xFC00
+        return (V(rng.standard_normal((1, 32, 128), dtype=np.float32), oracle.F32, *views.decoder_q(1, 32, 128)),
+                V(f16((cap, 8, 128)), oracle.F16, kne, knb), V(f16((cap, 8, 128)), oracle.F16, kne, knb),
+                V(mask, oracle.F16, *views.mask(n_kv, 1)), scale)
+    if kind == "batched":
+        # 32 streams of ragged length (the GPU leg's lengths), cache rows past
+        # a stream's length are never read (their mask entries are -inf)
+        B, cap = 32, 8192
+        import torch
+        g = torch.Generator(device="cpu")
+        g.manual_seed(5)
+        lens = torch.randint(512, 8193, (B,), generator=g).numpy()
+        k = np.zeros((B, cap, 8, 128), dtype=np.uint16)
+        v = np.zeros((B, cap, 8, 128), dtype=np.uint16)
+        mask = np.full((B, cap), 0xFC00, dtype=np.uint16)
+        for b in range(B):
+            k[b, : lens[b]] = f16((int(lens[b]), 8, 128), 0.5)
+            v[b, : lens[b]] = f16((int(lens[b]), 8, 128), 0.5)
+            mask[b, : lens[b]] = 0
+        qne, qnb = views.decoder_q(1, 32, 128)
+        qne, qnb = (qne[0], qne[1], qne[2], B), (qnb[0], qnb[1], qnb[2], 32 * 128 * 4)
+        kne, knb = views.kv_cache(cap, 8, 128, cap, batch=B)
+        return (V(rng.standard_normal((B, 1, 32, 128), dtype=np.float32), oracle.F32, qne, qnb),
+                V(k, oracle.F16, kne, knb), V(v, oracle.F16, kne, knb),
+                V(mask, oracle.F16, *views.mask(cap, 1, 1, B)), scale)
+    raise ValueError(kind)
+
+
+# configuration -> (input kind, calls timed per repetition, repetitions)
+CPU_SAMPLES = {
+    "encoder_prefill_1500x20_hd64": ("encoder", 1, 9),
+    "decode_nkv1024": ("decode1024", 20, 9),
+    "decode_nkv8192": ("decode8192", 5, 9),
+    "decoder_prefill_439_causal": ("prefill439", 1, 9),
+    "sliding_window_decode_16k_w2048": ("sliding", 5, 9),
+    "batched_ragged_32_streams": ("batched", 1, 9),
+}
+
+
+def cpu_baselines():
+    """Median µs per call of every configuration through the vectorised CPU
+    restatement, at min(hw, 16) threads (voxtral's default,
+    src/voxtral.cpp:1046-1051) and at every hardware thread of this process."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+    t_def, t_all = oracle.default_threads(), oracle.host_threads()
+    res = {}
+    total = 0.0
+    for name, (kind, calls, reps) in CPU_SAMPLES.items():
+        q, k, v, m, scale = _cpu_inputs(kind, seed=11 + len(res))
+        out = None
+        row = {}
+        for label, thr in (("default", t_def), ("all", t_all)):
+            out = oracle.fa_cpu_simd(q, k, v, m, scale, threads=thr, out=out)   # warm-up
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                for _ in range(calls):
+                    oracle.fa_cpu_simd(q, k, v, m, scale, threads=thr, out=out)
+                times.append((time.perf_counter() - t0) / calls)
+                total += times[-1] * calls
+            row[f"us_per_call_{label}"] = float(np.median(times)) * 1e6
+            row[f"threads_{label}"] = thr
+        row["sample"] = f"{calls} call(s) x {reps} repetitions per thread count, median"
+        res[name] = row
+        log(f"[cpu] {name}: {row['us_per_call_default']:.0f} us ({t_def} threads), "
+            f"{row['us_per_call_all']:.0f} us ({t_all} threads)")
+    return res, t_def, t_all, total
+
+
+def stream_read_ceiling(torch, steps, warmup):
+    """Reference rate for the decode kernels: a plain read-only stream
+    (bench_stream.hip: 16-byte loads, eight in flight per thread, 512
+    workgroups) over 30 distinct 32 MiB buffers (a decode layer's K/V bytes
+    at n_kv 8192; 1 GB in all, past the 256 MB MALL), one launch per buffer,
+    replayed from a HIP graph like the decode layers, so it pays the same
+    per-launch ramp and tail. Reported as GB/s of buffer bytes."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "bench_stream.so"))
+    lib.bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    n, nbytes = 30, 32 << 20
+    bufs = [torch.ones(nbytes // 4, device="cuda", dtype=torch.float32) for _ in range(n)]
+    out = torch.zeros(4, device="cuda", dtype=torch.int32)
+    stream = torch.cuda.Stream()
+
+    def step():
+        for b in bufs:
+            if lib.bench_stream_read(b.data_ptr(), nbytes, out.data_ptr(), stream.cuda_stream):
+                raise RuntimeError("bench_stream_read launch failed")
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, warmup)):
+            step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        g.replay()
+        start.record(stream)
+        for _ in range(steps):
+            g.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / (steps * n)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[hbm read ceiling] 32 MiB read-only stream: {us:.2f} us, {gbs:.0f} GB/s")
+    del g, bufs
+    torch.cuda.empty_cache()
+    return {"us_per_32MiB": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+            "method": "bench_stream.hip read-only stream over 30 distinct 32 MiB buffers, HIP-graph replay, "
+                      "one launch per buffer"}
 
 
 def load_traffic(kernel_prefix):
@@ -267,26 +395,6 @@ def calib_copy(torch, mib=256, reps=3):
         b.copy_(a)
     torch.cuda.synchronize()
     log(f"[calib] copied {mib} MiB x {reps}")
-
-
-def cpu_decode_us(n_kv=8192):
-    import numpy as np
-    sys.path.insert(0, ROOT)
-    from oracle import oracle
-    rng = np.random.default_rng(8)
-    q = rng.standard_normal((1, 32, 128), dtype=np.float32)
-    k = rng.standard_normal((n_kv, 8, 128), dtype=np.float32).astype(np.float16).view(np.uint16)
-    v = rng.standard_normal((n_kv, 8, 128), dtype=np.float32).astype(np.float16).view(np.uint16)
-    qv = oracle.View(q, oracle.F32, *views.decoder_q(1, 32, 128))
-    kne, knb = views.kv_cache(n_kv, 8, 128, n_kv)
-    kv, vv = oracle.View(k, oracle.F16, kne, knb), oracle.View(v, oracle.F16, kne, knb)
-    threads = oracle.default_threads()
-    oracle.fa_ggml(qv, kv, vv, None, f32s(1 / math.sqrt(128)), vkq_f16=True, threads=threads)
-    reps = 5
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        oracle.fa_ggml(qv, kv, vv, None, f32s(1 / math.sqrt(128)), vkq_f16=True, threads=threads)
-    return (time.perf_counter() - t0) / reps * 1e6, threads
 
 
 # ---------------------------------------------------------------------------
@@ -330,7 +438,13 @@ def main():
     del enc
     torch.cuda.empty_cache()
 
-    if want("decode"):
+    # --only decode_plain: just the plain decode layers (n_kv 1024 and 8192),
+    # for counter runs that must tell those kernels apart
+    plain_only = only is not None and "decode_plain" in only
+    if want("decode") or want("ceiling") or plain_only:
+        configs["hbm_read_ceiling"] = stream_read_ceiling(torch, K, W)
+
+    if want("decode") or plain_only:
         # cold: enough distinct layer caches that one step's reads exceed the
         # 256 MB MALL (n_kv 1024: 80 x 4.2 MB; n_kv 8192: 30 x 33.6 MB)
         for n_kv, layers in ((1024, 80), (8192, 30)):
@@ -339,11 +453,13 @@ def main():
             by = decode_bytes(n_kv)
             gbs = by / (us * 1e-6) / 1e9
             log(f"[decode n_kv={n_kv}] {us:.2f} us/layer  {gbs:.0f} GB/s")
+            ceil = configs.get("hbm_read_ceiling", {}).get("gbs")
             configs[f"decode_nkv{n_kv}"] = {"us_per_layer": us, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                                            "frac_read_ceiling": gbs / ceil if ceil else None,
                                             "bytes_per_layer": by, "layers": layers,
                                             "cache": f"cold ({layers} layer caches, {layers * by / 1e6:.0f} MB "
                                                      "per step > 256 MB MALL)"}
-            if n_kv == 8192:
+            if n_kv == 8192 and not plain_only:
                 # the new token's K/V (F32, one 1024-float row each) appended to the f16 cache:
                 # fused into the attention launch, and as a separate append launch
                 news = [(randn(torch, (1024,), 7000 + 2 * i), randn(torch, (1024,), 7001 + 2 * i))
@@ -370,6 +486,7 @@ def main():
                 del news
             del dl
             torch.cuda.empty_cache()
+    if want("decode"):
         # the reference's own F32 cache (src/voxtral.cpp:1126-1136), read in place
         dl = decode_layers(torch, 30, 8192, seed=2500, kv_f32=True)
         _, us = time_calls(torch, ctx, dl, K, W)
@@ -474,12 +591,28 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log("[cpu baseline] encoder layer on host cores ...")
-        cpu = cpu_baseline_encoder()
-        us_cpu_dec, thr = cpu_decode_us(8192)
-        configs.setdefault("decode_nkv8192", {})["cpu_us_per_layer"] = us_cpu_dec
-        configs["encoder_prefill_1500x20_hd64"]["cpu_us_per_layer"] = cpu.pop("us_per_layer")
-        log(f"[cpu baseline] {cpu['value']*1e3:.2f} GFLOP/s encoder, decode 8192 {us_cpu_dec:.0f} us, {thr} threads")
+        log("[cpu baseline] every configuration on the host cores ...")
+        rows, t_def, t_all, total = cpu_baselines()
+        for name, row in rows.items():
+            c = configs.setdefault(name, {})
+            c["cpu_us_per_call"] = row["us_per_call_default"]
+            c["cpu_us_per_call_all_threads"] = row["us_per_call_all"]
+            gpu_us = c.get("us_per_layer", c.get("us_per_step_cold", c.get("us_per_call")))
+            if gpu_us:
+                c["speedup_vs_cpu"] = row["us_per_call_default"] / gpu_us
+        enc_us = rows["encoder_prefill_1500x20_hd64"]["us_per_call_default"]
+        cpu = {"value": flops_enc / (enc_us * 1e-6) / 1e12, "unit": "TFLOP/s", "cores": t_def, "kind": "port",
+               "sample": "every configuration: encoder 1500x20 hd64 (one layer), decode n_kv 1024 and 8192, "
+                         "decoder prefill 439 causal, one sliding-window step (n_kv 16335, window 2048), the "
+                         "32-stream ragged batch; median of 9 repetitions per call through oracle/fa_cpu_simd.c "
+                         "(ggml's one-row algorithm with AVX2/F16C vector kernels, f16 V accumulation), "
+                         f"{total:.1f} s of CPU work",
+               "threads_default": t_def, "threads_all": t_all,
+               "value_all_threads": flops_enc / (rows["encoder_prefill_1500x20_hd64"]["us_per_call_all"] * 1e-6)
+               / 1e12,
+               "configs": rows}
+        log(f"[cpu baseline] encoder {cpu['value']*1e3:.1f} GFLOP/s at {t_def} threads, "
+            f"{cpu['value_all_threads']*1e3:.1f} GFLOP/s at {t_all} threads")
 
     ms_step, us_layer, tflops = headline
     line = {

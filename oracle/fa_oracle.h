@@ -55,6 +55,14 @@ int oracle_fa_f64(const vxfa_tensor* q, const vxfa_tensor* k,
                   double* dst, float scale, float max_bias,
                   float logit_softcap, int q_f16, int n_threads);
 
+/* The same one-row algorithm with ggml-cpu's AVX2 / F16C vector kernels
+ * (fa_cpu_simd.c): the CPU baseline bench.py times. F16 K and V, F32 or F16
+ * Q, optional F16 mask; V accumulated in f16 as ggml's one-row kernel does.
+ * Returns 0, or -1 on a contract violation. */
+int oracle_fa_cpu_simd(const vxfa_tensor* q, const vxfa_tensor* k,
+                       const vxfa_tensor* v, const vxfa_tensor* mask,
+                       vxfa_tensor* dst, float scale, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,15 +79,25 @@ def lib():
         L.oracle_fa_f64.argtypes = [P, P, P, P, ctypes.POINTER(ctypes.c_double), ctypes.c_float,
                                     ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_int]
         L.oracle_fa_f64.restype = ctypes.c_int
+        L.oracle_fa_cpu_simd.argtypes = [P, P, P, P, P, ctypes.c_float, ctypes.c_int]
+        L.oracle_fa_cpu_simd.restype = ctypes.c_int
         L.oracle_f32_to_f16_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         L.oracle_f16_to_f32_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         _lib = L
     return _lib
 
 
+def host_threads() -> int:
+    """Hardware threads this process may run on (its CPU affinity set)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        return max(1, os.cpu_count() or 1)
+
+
 def default_threads() -> int:
     """voxtral's default: min(hardware threads, 16) (src/voxtral.cpp:1046-1051)."""
-    return max(1, min(os.cpu_count() or 4, 16))
+    return max(1, min(host_threads(), 16))
 
 
 def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
@@ -126,6 +136,25 @@ def fa_ggml(q: View, k: View, v: View, mask: View | None, scale: float,
                               threads if threads else default_threads())
     if rc != 0:
         raise ValueError("oracle_fa_ggml: contract violation")
+    return out
+
+
+def fa_cpu_simd(q: View, k: View, v: View, mask: View | None, scale: float,
+                threads: int | None = None, out: np.ndarray | None = None) -> np.ndarray:
+    """ggml's one-row algorithm with its AVX2/F16C vector kernels (the timed
+    CPU baseline); returns float32 [B, Nq, Hq, DV]."""
+    shape = _out_shape(q, v)
+    if out is None:
+        out = np.zeros(shape, dtype=np.float32)
+    DV, Hq, Nq, B = shape[3], shape[2], shape[1], shape[0]
+    dst = View(out, F32, (DV, Hq, Nq, B), (4, 4 * DV, 4 * DV * Hq, 4 * DV * Hq * Nq))
+    qd, kd, vd, dd = q.desc(), k.desc(), v.desc(), dst.desc()
+    md = mask.desc() if mask is not None else None
+    rc = lib().oracle_fa_cpu_simd(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd),
+                                  ctypes.byref(md) if md is not None else None, ctypes.byref(dd),
+                                  scale, threads if threads else default_threads())
+    if rc != 0:
+        raise ValueError("oracle_fa_cpu_simd: contract violation")
     return out
 
 

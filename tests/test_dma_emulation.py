@@ -1,0 +1,44 @@
+"""CPU emulation of the LDS-DMA copy schedule of the hd 64 encoder kernel
+(fa_prefill_pp.hip): global source ranges, LDS targets and the s_waitcnt
+vmcnt accounting against the barriers, for every KV group and wavefront of
+each shape and both workgroup shapes (see tests/dma_emul.py). Runs without a
+GPU."""
+import pytest
+
+from dma_emul import Mem, Shape, Violation, emulate_pp, pp_copy
+
+# the encoder configuration, every encoder length the GPU tests use, GQA,
+# batches, empty KV groups (n_kv < 4 blocks), partial last blocks and wide
+# row strides (a K/V view inside a larger cache)
+SHAPES = [Shape(1500, 1500, 20, 20)] + [Shape(n, n, 4, 4) for n in (1, 2, 31, 32, 33, 64, 96, 128, 161, 300, 700)] + [
+    Shape(1024, 1024, 3, 3), Shape(257, 257, 8, 2), Shape(200, 97, 4, 4, b=3, bk=3),
+    Shape(129, 4097, 2, 2), Shape(64, 1500, 2, 1, k_nb1=(8 << 20) - 16, v_nb1=(8 << 20) - 16),
+]
+
+
+@pytest.mark.parametrize("sh", SHAPES, ids=lambda s: f"nq{s.nq}_nkv{s.nkv}_h{s.hq}x{s.hkv}_b{s.b}_nb{s.k_nb1}")
+@pytest.mark.parametrize("nqt,kvg,ns", [(2, 4, 4), (2, 2, 8)])
+def test_pp_copies_and_waits_in_bounds(sh, nqt, kvg, ns):
+    emulate_pp(sh, nqt, kvg, ns)
+
+
+def test_emulation_catches_planted_mistakes():
+    """The checks fire: a block read with one copy too many still in flight,
+    and a copy of the partial block without the row clamp."""
+    m = Mem()
+    for blk in (0, 1):
+        for _ in range(8):
+            m.issue(blk)
+    m.wait(9)   # one of block 0's copies still outstanding
+    assert not m.complete(0)
+    m.wait(8)
+    assert m.complete(0) and not m.complete(1)
+    sh = Shape(100, 100, 1, 1)
+    import dma_emul
+    orig = dma_emul.np.minimum
+    try:
+        dma_emul.np.minimum = lambda a, b: a   # drop the clamp of rows past n_kv
+        with pytest.raises(Violation):
+            pp_copy(sh, 2, 4, 4, 0, 0, 3, 0, Mem())   # block 3 = rows 96..127 of 100
+    finally:
+        dma_emul.np.minimum = orig
