@@ -11,9 +11,12 @@ show, for a given shape and stride set, that
     workgroup's LDS allocation,
   * every operand read from LDS (K 128-bit reads, V^T transposed 8-byte
     reads) stays inside the slot of the block it reads,
-  * the s_waitcnt vmcnt(N) before a block's first read leaves only copies of
-    later blocks in flight (vector-memory loads complete in issue order),
-  * no copy is issued into a slot whose block still has reads to come.
+  * every block is landed, in both wavefronts' halves, at the barrier
+    before the epoch that reads it (s_waitcnt vmcnt(N) leaves only younger
+    copies in flight: vector-memory loads complete in issue order),
+  * no copy is issued into a slot whose block still has reads to come (a
+    copy in epoch e may overwrite a block last read in an earlier epoch),
+  * every wavefront passes the same number of barriers.
 
 Nothing here runs on a GPU; the formulas are the kernels' own, so a change to
 a kernel's indexing has to be mirrored here for the test to stay meaningful.
@@ -92,8 +95,8 @@ class Mem:
 
 
 # ---------------------------------------------------------------------------
-# fa_prefill_pp.hip (Shape<NQT, KVG, NS>): a shared ring per KV group, one
-# barrier per block; wavefront (kg, wq) copies rows 8 (NQT i + wq) + l / 8
+# fa_prefill_pp.hip: KVG groups x NQT query tiles, an NS-slot ring per group;
+# wavefront (kg, wq) copies rows 8 (NQT i + wq) + l / 8 of each block
 
 def pp_copy(sh: Shape, NQT, KVG, NS, kg, wq, bs, blk, mem: Mem):
     BLK = 32 * 128
@@ -120,46 +123,90 @@ def pp_copy(sh: Shape, NQT, KVG, NS, kg, wq, bs, blk, mem: Mem):
             mem.issue(blk)
 
 
-def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4):
+def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4, plant=None):
+    """The kernel's copy schedule, epoch by epoch (epoch e runs between
+    barrier e and barrier e + 1; the prologue's barrier is barrier 0 and
+    iteration t of the main loop runs in epoch t).
+
+    plant (tests only): "wait_late" waits for one block fewer at the end of
+    each iteration, "copy_early" copies block t + NS + 1 in iteration t."""
     BM = 64 * NQT
     NLD = 4 // NQT
-    nqg = (sh.nq + BM - 1) // BM
     nblk = (sh.nkv + 31) // 32
     ni = (nblk + KVG - 1) // KVG
-    AHEAD = NS - 1
+    ahead = NS + 1 if plant == "copy_early" else NS
+    slack = 1 if plant == "wait_late" else 0
     for kg in range(KVG):
         bs = min(kg * ni, nblk)
         ng = min(ni, nblk - bs)
         part = ng > 0 and (bs + ng) * 32 > sh.nkv
         nf = ng - (1 if part else 0)
-        mems = []
-        for wq in range(NQT):
-            mem = Mem()
+        mems = [Mem() for _ in range(NQT)]
+        copy_epoch = {}                      # block -> epoch its copies were issued in
+        done_by = [dict() for _ in range(NQT)]   # block -> barrier by which this wavefront's copy had landed
+        reads = []                           # (epoch, block)
+        nbar = 0
+
+        def copy(blk, epoch):
+            for wq in range(NQT):
+                pp_copy(sh, NQT, KVG, NS, kg, wq, bs, blk, mems[wq])
+            _check(blk not in copy_epoch, f"block {blk} copied twice")
+            copy_epoch[blk] = epoch
+
+        def wait_all(k):                     # every wavefront: at most k blocks in flight
+            for mem in mems:
+                mem.wait(k * 2 * NLD)
+
+        def barrier():
+            nonlocal nbar
+            for wq in range(NQT):
+                for blk in copy_epoch:
+                    if blk not in done_by[wq] and mems[wq].complete(blk):
+                        done_by[wq][blk] = nbar
+            nbar += 1
+
+        # prologue: Q, then blocks 0 .. NS - 2
+        npre = min(ng, NS - 1)
+        for mem in mems:
             for _ in range(BM * 16 // (64 * NQT * KVG)):
                 mem.issue("Q")
-            npre = min(ng, AHEAD)
-            for blk in range(npre):
-                pp_copy(sh, NQT, KVG, NS, kg, wq, bs, blk, mem)
+        for blk in range(npre):
+            copy(blk, -1)
+        for mem in mems:
             mem.wait(min(npre, 8) * 2 * NLD)
             _check(mem.complete("Q"), "Q staged before its loads completed")
-            mem.wait(max(npre - 2, 0) * 2 * NLD)
-            mems.append((mem, npre))
-        # barrier: blocks 0 and 1 visible to every wavefront of the group
-        for b0 in range(min(2, ng)):
-            _check(all(m.complete(b0) for m, _ in mems), f"block {b0} not landed at the prologue barrier")
-        for t in range(0, max(nf - 1, 0)):
-            for wq, (mem, _) in enumerate(mems):
-                if t + AHEAD < ng:
-                    pp_copy(sh, NQT, KVG, NS, kg, wq, bs, t + AHEAD, mem)
-                mem.wait(max(min(t + AHEAD, ng - 1) - (t + 2), 0) * 2 * NLD)
-            # barrier; block t + 1 is read at the top of the next iteration and
-            # must be complete in every wavefront's copies (t + 2 for the one after)
-            for b1 in (t + 1, t + 2):
-                if b1 < ng:
-                    _check(all(m.complete(b1) for m, _ in mems), f"block {b1} not landed at barrier {t}")
-            # the slot refilled at iteration t held block t - 1, last read in iteration t - 1
-            if t + AHEAD < ng:
-                _check((t + AHEAD) % NS == (t - 1) % NS or t == 0, "refill of a live slot")
-        for mem, _ in mems:
-            mem.wait(0)
+        wait_all(max(npre - 2, 0))
+        barrier()                            # barrier 0
+        if nf > 0:
+            reads += [(0, 0), (0, 0)]        # K_0, V_0
+        for t in range(nf - 1):              # epoch t
+            if t == 1 and NS < ng:
+                copy(NS, t)
+            reads.append((t, t + 1))         # K_{t+1}
+            mid = NS - 1 if t == 0 else t + ahead
+            if mid < ng:
+                copy(mid, t)
+            reads.append((t, t + 1))         # V_{t+1}
+            last = min(t + ahead if t >= 1 else NS - 1, ng - 1)
+            wait_all(max(last - (t + 2) + slack, 0))
+            barrier()
+        if nf > 0:
+            wait_all(0)
+            barrier()
+        if part:
+            reads += [(nbar - 1, nf)] * 2       # after the barrier that ends the last full block
+            barrier()
+        for _ in range(ng, ni):
+            barrier()
+        _check(nbar == 1 + ni, "barrier count differs from 1 + ni")
+        for epoch, blk in reads:
+            # both halves landed before the barrier that opened the epoch
+            for wq in range(NQT):
+                _check(done_by[wq].get(blk, 10 ** 9) <= epoch, f"block {blk} read in epoch {epoch} before it landed")
+            # the slot still holds the block: the slot's next block is copied
+            # in a later epoch
+            nxt = blk + NS
+            if nxt in copy_epoch:
+                _check(copy_epoch[nxt] > epoch, f"block {blk} overwritten before its read in epoch {epoch}")
+        _check(len(copy_epoch) == ng, "not every block of the group was copied")
     return {"nblk": nblk}

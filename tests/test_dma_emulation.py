@@ -1,8 +1,7 @@
 """CPU emulation of the LDS-DMA copy schedule of the hd 64 encoder kernel
 (fa_prefill_pp.hip): global source ranges, LDS targets and the s_waitcnt
 vmcnt accounting against the barriers, for every KV group and wavefront of
-each shape and both workgroup shapes (see tests/dma_emul.py). Runs without a
-GPU."""
+each shape (see tests/dma_emul.py). Runs without a GPU."""
 import pytest
 
 from dma_emul import Mem, Shape, Violation, emulate_pp, pp_copy
@@ -17,9 +16,16 @@ SHAPES = [Shape(1500, 1500, 20, 20)] + [Shape(n, n, 4, 4) for n in (1, 2, 31, 32
 
 
 @pytest.mark.parametrize("sh", SHAPES, ids=lambda s: f"nq{s.nq}_nkv{s.nkv}_h{s.hq}x{s.hkv}_b{s.b}_nb{s.k_nb1}")
-@pytest.mark.parametrize("nqt,kvg,ns", [(2, 4, 4), (2, 2, 8)])
-def test_pp_copies_and_waits_in_bounds(sh, nqt, kvg, ns):
-    emulate_pp(sh, nqt, kvg, ns)
+def test_pp_copies_and_waits_in_bounds(sh):
+    emulate_pp(sh)
+
+
+@pytest.mark.parametrize("plant", ["wait_late", "copy_early"])
+def test_schedule_emulation_catches_planted_mistakes(plant):
+    """A wait one block short, or a copy one block further ahead (into the
+    slot of a block still to be read), is reported."""
+    with pytest.raises(Violation):
+        emulate_pp(Shape(1500, 1500, 20, 20), plant=plant)
 
 
 def test_emulation_catches_planted_mistakes():

@@ -63,6 +63,52 @@ struct AttnArgs {
     int64_t kn_nb3, vn_nb3;
 };
 
+// n / d for 0 <= n < 2^31 by a multiply-high, an add and a shift, with the
+// constants computed on the host (Granlund and Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994: s = ceil(log2 d),
+// m = floor(2^32 (2^s - d) / d) + 1, n / d = (mulhi(n, m) + n) >> s, where
+// the sum stays below 2^32 because mulhi(n, m) < n < 2^31).
+struct FastDiv {
+    uint32_t m, s;
+    static FastDiv make(uint32_t d) {   // d >= 1
+        uint32_t s = 0;
+        while ((1ull << s) < d) ++s;
+        const uint64_t m = (((1ull << s) - d) << 32) / d + 1;
+        return FastDiv{(uint32_t)m, s};
+    }
+    __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        return (uint32_t)((((uint64_t)n * m) >> 32) + n) >> s;
+    }
+};
+
+// Workgroup -> (query tile, head, batch, kv head, kv batch) of a prefill
+// grid of nwg = nqt * hq * b workgroups. Workgroups are dealt to the 8 XCDs
+// round robin (blockIdx % 8), so logical index gidx is laid out to give each
+// XCD a contiguous range: consecutive query tiles of one head then share that
+// XCD's L2 for the head's K and V. All constants come from the host, so the
+// kernel's first global loads wait on one batch of argument loads and no
+// division.
+struct GridMap {
+    uint32_t q8, r8;          // nwg / 8, nwg % 8
+    uint32_t nqt, hq;
+    FastDiv by_nqt, by_hq, by_grp, by_bgrp;   // grp = hq / hkv, bgrp = b / bk
+    static GridMap make(int nwg, int nqt, int hq, int hkv, int b, int bk) {
+        return GridMap{(uint32_t)nwg >> 3, (uint32_t)nwg & 7, (uint32_t)nqt, (uint32_t)hq,
+                       FastDiv::make(nqt), FastDiv::make(hq), FastDiv::make(hq / hkv), FastDiv::make(b / bk)};
+    }
+    __host__ __device__ __forceinline__ void locate(uint32_t lin, int& qt, int& h, int& b, int& hk, int& bkv) const {
+        const uint32_t xcd = lin & 7;
+        const uint32_t gidx = (xcd < r8 ? xcd : r8) * (q8 + 1) + (xcd > r8 ? xcd - r8 : 0u) * q8 + (lin >> 3);
+        const uint32_t t = by_nqt.div(gidx);
+        const uint32_t bb = by_hq.div(t);
+        qt = (int)(gidx - t * nqt);
+        h = (int)(t - bb * hq);
+        b = (int)bb;
+        hk = (int)by_grp.div((uint32_t)h);
+        bkv = (int)by_bgrp.div(bb);
+    }
+};
+
 // F32 -> F16 append of new K/V rows into the cache (the ggml_cpy of
 // src/voxtral.cpp:1758-1770 into an f16 cache).
 struct AppendArgs {
@@ -336,7 +382,7 @@ constexpr int kDecodeWaves = 4;      // wavefronts per decode workgroup
 // a multiple of 4 so every record starts 16-byte aligned.
 constexpr int dec_record_floats(int D, int G) { return G * D + ((2 * G + 3) & ~3); }
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
-hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t stream);
+hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
 // F32 -> f16 copy of a [D, n, H, B] view (byte strides nb1..nb3, rows

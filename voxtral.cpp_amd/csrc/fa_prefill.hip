@@ -231,7 +231,7 @@ __device__ __forceinline__ void mask_scan_tiles(const uint16_t* base, int64_t ro
 // mixed tile's mask words are formed in registers, bit for bit those the
 // tensor would give.
 template <int D, int NQW, int KVG, int MM, bool QF16>
-__global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, int nqt) {
+__global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, GridMap gm) {
     static_assert(D == 64 || D == 128, "head dim");
     constexpr bool MASK = MM != 0;
     constexpr bool IMPL = MM == 2;
@@ -258,13 +258,8 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     __shared__ uint8_t s_tflag[MM == 1 ? NQW * PF_MAXT : 1];
 
     // ---- XCD-aware position of this workgroup --------------------------------
-    const int nwg = gridDim.x;
-    const int lin = blockIdx.x;
-    const int xcd = lin & 7, q8 = nwg >> 3, r8 = nwg & 7;
-    const int gidx = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + (lin >> 3);
-    const int qt = gidx % nqt;
-    const int h = (gidx / nqt) % a.hq;
-    const int b = gidx / (nqt * a.hq);
+    int qt, h, b, hk, bkv;
+    gm.locate(blockIdx.x, qt, h, b, hk, bkv);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -272,10 +267,6 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     const int qw = wave % NQW;
     const int kg = wave / NQW;
     const int q0 = qt * BM;
-    // (uniform; computed on the vector unit, so moved to scalar registers
-    // for the K/V row addresses, which the LDS copies take as scalars)
-    const int hk = __builtin_amdgcn_readfirstlane(h / (a.hq / a.hkv));
-    const int bkv = __builtin_amdgcn_readfirstlane(b / (a.b / a.bk));
     const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
 
@@ -383,7 +374,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         return s + 1 < step_hi ? s + 1 : -1;
     };
     int first = -1;
-    if (!MASK) first = nstep == 1 ? 0 : (int)(((int64_t)qt * (nstep - 1)) / nqt);
+    if (!MASK) first = nstep == 1 ? 0 : (int)(((int64_t)qt * (nstep - 1)) / (int)gm.nqt);
     else if (step_lo < step_hi) first = step_lo;
 
     // ---- step loads: global -> LDS ------------------------------------------
@@ -770,9 +761,10 @@ static hipError_t launch_pw(const AttnArgs& a, hipStream_t st) {
     const int64_t nwg = (int64_t)nqt * a.hq * a.b;
     if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
     constexpr int NT = 64 * NQW * KVG;
+    const GridMap gm = GridMap::make((int)nwg, nqt, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
-    if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, true>), grid, block, 0, st, a, nqt);
-    else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, false>), grid, block, 0, st, a, nqt);
+    if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, true>), grid, block, 0, st, a, gm);
+    else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, false>), grid, block, 0, st, a, gm);
     return hipGetLastError();
 }
 

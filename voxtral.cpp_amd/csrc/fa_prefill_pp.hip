@@ -7,16 +7,21 @@
 // mask = null, scale = 1/sqrt(64) (src/voxtral.cpp:1580-1613, FA at :1611).
 //
 // Work decomposition
-//   Workgroup = NQT query tiles of 64 rows x KVG KV groups, one wavefront
-//   each. KV group g walks its own contiguous share of the 32-position
-//   blocks; the groups' partial (O, m, l) are merged through LDS at the end.
-//   Two shapes: Shape1 = 2 x 2 (4 wavefronts, one per SIMD, 8-slot ring) and
-//   Shape2 = 2 x 4 (8 wavefronts, two per SIMD, 4-slot ring), the default:
-//   the second wavefront on a SIMD covers the first one's memory and
-//   dependency stalls (26.5 against 28.3 us per encoder layer). At 1500 x 20
-//   the grid is 12 x 20 = 240 workgroups, one per CU. The workgroups of one
-//   head are dealt to one XCD (workgroups go to the 8 XCDs round robin), so
-//   that head's K/V stays in one L2.
+//   Workgroup = 2 query tiles of 64 rows x 4 KV groups, one wavefront each
+//   (8 wavefronts, two per SIMD). KV group g walks its own contiguous share
+//   of the 32-position blocks; the groups' partial (O, m, l) are merged
+//   through LDS at the end. At 1500 x 20 the grid is 12 x 20 = 240
+//   workgroups, one per CU. The workgroups of one head are dealt to one XCD
+//   (workgroups go to the 8 XCDs round robin), so that head's K/V stays in
+//   one L2.
+// Why two wavefronts per SIMD: one wavefront issues VALU instructions at
+//   about half the SIMD's rate and MFMAs at about 3/4 of the matrix pipe's;
+//   two interleaved streams fill both (measured: 1 MFMA + 6 VALU per
+//   wavefront runs at 72 cycles per MFMA with two wavefronts, the MFMA pipe
+//   75 % busy). Handing the matrix pipe and the VALU to the two wavefronts
+//   in turn (one runs all the MFMAs of a block while the other runs its
+//   softmax) measured slower (28.2 against 24.9 us per encoder layer): the
+//   softmax then runs at one wavefront's VALU rate.
 // Why 64 query rows per wavefront: every K and V operand read from LDS feeds
 //   two MFMAs (one per 32-row half), half the LDS reads per FLOP of a 32-row
 //   wavefront, whose operand reads alone would need the full LDS bandwidth
@@ -24,29 +29,30 @@
 // Register budget: all of a wavefront's state (O, Q, S, P, K and V operands
 //   of both halves, 200-230 VGPRs) stays in registers with no copies, which
 //   fits two wavefronts per SIMD (256 VGPRs each).
-// Ping-pong inside the wavefront: the halves A (rows 0-31) and B (rows 32-63)
-//   run half an iteration apart. Iteration t (block t of the group):
+// Two halves in flight inside the wavefront: the halves A (rows 0-31) and B
+//   (rows 32-63) run half an iteration apart. Iteration t (block t of the
+//   group):
 //     H1: MFMA  O_A += V_t^T P_A(t)^T, S_A(t+1) = K_{t+1} Q_A^T
 //         VALU  softmax of S_B(t) -> P_B(t)
 //     H2: MFMA  O_B += V_t^T P_B(t)^T, S_B(t+1) = K_{t+1} Q_B^T
 //         VALU  softmax of S_A(t+1) -> P_A(t+1)
 //   The MFMAs of a half do not depend on that half's VALU work, so the
 //   scheduler interleaves them. K_{t+1} is read at the top of iteration t
-//   (its block becomes visible at the barrier before); the softmax of S_B(t)
-//   does not need it, so the VALU (the busier pipe for hd 64) can start
-//   while the reads land. V_{t+1} is read in H2 of iteration t, once PV_B(t)
-//   has taken V_t's registers as operands: its block has been visible since
-//   the barrier before iteration t, and the transposed reads (half the LDS
-//   read rate of 128-bit ones) land under H2's work instead of after the
-//   next barrier.
-// K/V staging: an NS-slot LDS ring; block b sits in slot b % NS, its K is
-//   read at the top of iteration b - 1 and its V in iteration b - 1 as well;
-//   block b + NS - 1 goes into the slot of block b - 1 at the start of
-//   iteration b, one barrier after that block's last read
-//   (global_load_lds_dwordx4, no staging registers). A block therefore has
-//   NS - 3 iterations to arrive; at the end of iteration t each wavefront
-//   waits only for its own loads of block t + 2 (s_waitcnt vmcnt counting the
-//   younger blocks still in flight), then one barrier.
+//   (its block becomes visible at the barrier before) and lands under the
+//   PV MFMAs of H1, whose operands are already in registers. V_{t+1} is read
+//   in H2 of iteration t, once PV_B(t) has taken V_t's registers as
+//   operands.
+// K/V staging: a 4-slot LDS ring per KV group; block b sits in slot b % 4
+//   and is read (K and V) in iteration b - 1. Block t + 4 is copied into the
+//   slot of block t in the middle of iteration t, one barrier after block
+//   t's last read (global_load_lds_dwordx4, no staging registers; between
+//   the halves, so the copy instructions queue at the texture unit while the
+//   MFMAs of H1 run rather than all 8 wavefronts' at once after a barrier);
+//   block 4 goes in at the top of iteration 1 (block 0 is read after the
+//   prologue's barrier). A block has 2.5 iterations to arrive: at the end of
+//   iteration t each wavefront waits only for its own loads of block t + 2
+//   (s_waitcnt vmcnt counting the younger blocks still in flight), then one
+//   barrier.
 // Q is loaded coalesced by the whole workgroup, rounded to f16 and staged in
 //   LDS; the output goes out through LDS as full 256-byte rows.
 // LDS rows and swizzles, MFMA operand layouts and the row-to-KV permutation
@@ -74,27 +80,19 @@ constexpr int GRP = 2 * BLK;        // K then V of one group in a ring slot
 constexpr float TAU = 8.0f;
 
 // Workgroup shape: NQT query tiles of 64 rows x KVG KV groups (one wavefront
-// each), an NS-slot LDS ring.
-template <int NQT_, int KVG_, int NS_>
-struct Shape {
-    static constexpr int NQT = NQT_;
-    static constexpr int KVG = KVG_;
-    static constexpr int NS = NS_;
-    static constexpr int NW = NQT * KVG;        // wavefronts
-    static constexpr int NT = 64 * NW;
-    static constexpr int BM = 64 * NQT;         // query rows per workgroup
-    static constexpr int AHEAD = NS - 1;        // blocks loaded ahead of the one computed
-    static constexpr int SLOT = KVG * GRP;
-    static constexpr int RING = NS * SLOT;
-    static constexpr int QST = BM * ROW;        // Q staging: BM rows of 64 f16
-    static constexpr int NLD = 4 / NQT;         // K (and V) load instructions per wavefront per block
-    static constexpr int PUB = 2 * 32 + 4;      // floats each wavefront publishes per lane for the merge
-    static constexpr int XS = KVG * NQT * PUB * 64 * 4;       // merge area (then the output staging tile)
-};
-// one wavefront per SIMD (4 wavefronts, 8-slot ring)
-using Shape1 = Shape<2, 2, 8>;
-// two wavefronts per SIMD (8 wavefronts, 4-slot ring)
-using Shape2 = Shape<2, 4, 4>;
+// each), an NS-slot LDS ring per group.
+constexpr int NQT = 2;
+constexpr int KVG = 4;
+constexpr int NS = 4;
+constexpr int NW = NQT * KVG;        // wavefronts
+constexpr int NT = 64 * NW;
+constexpr int BM = 64 * NQT;         // query rows per workgroup
+constexpr int SLOT = KVG * GRP;
+constexpr int RING = NS * SLOT;
+constexpr int QST = BM * ROW;        // Q staging: BM rows of 64 f16
+constexpr int NLD = 4 / NQT;         // K (and V) load instructions per wavefront per block
+constexpr int PUB = 2 * 32 + 4;      // floats each wavefront publishes per lane for the merge
+constexpr int XS = KVG * NQT * PUB * 64 * 4;   // merge area (then the output staging tile)
 }  // namespace pp
 
 // s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
@@ -105,6 +103,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
+
+// every LDS read of this wavefront has returned (s_waitcnt lgkmcnt(0))
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // wait until at most k blocks' loads (2 NLD instructions each) are in flight
 template <int NLD>
@@ -123,24 +124,17 @@ __device__ __forceinline__ void wait_blocks(int k) {
     }
 }
 
-template <class SH, bool QF16, bool C8>
-__global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, int nblk, int ni) {
+template <bool QF16, bool C8>
+__global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm, int nblk, int ni) {
     using namespace pp;
-    constexpr int NQT = SH::NQT, KVG = SH::KVG, NS = SH::NS, NT = SH::NT, BM = SH::BM;
-    constexpr int AHEAD = SH::AHEAD, SLOT = SH::SLOT, RING = SH::RING, QST = SH::QST, NLD = SH::NLD;
     static_assert(NLD * NQT == 4, "a block's 4 load instructions per matrix split evenly");
     static_assert(8 * 2 * NLD < 64 && NS <= 8, "vmcnt range of wait_blocks");
-    static_assert(SH::XS <= RING + QST && BM * 256 <= RING + QST, "merge and output staging fit the LDS");
+    static_assert(XS <= RING + QST && BM * 256 <= RING + QST, "merge and output staging fit the LDS");
     __shared__ __attribute__((aligned(16))) char smem[RING + QST];
 
     // ---- XCD-aware position of this workgroup --------------------------------
-    const int nwg = gridDim.x;
-    const int lin = blockIdx.x;
-    const int xcd = lin & 7, q8 = nwg >> 3, r8 = nwg & 7;
-    const int gidx = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + (lin >> 3);
-    const int qg = gidx % nqg;
-    const int h = (gidx / nqg) % a.hq;
-    const int b = gidx / (nqg * a.hq);
+    int qg, h, b, hk, bkv;
+    gm.locate(blockIdx.x, qg, h, b, hk, bkv);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -150,8 +144,6 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     const int nl = lane & 31;
     const int hh = lane >> 5;
     const int qw0 = qg * BM;                  // first query row of the workgroup
-    const int hk = h / (a.hq / a.hkv);
-    const int bkv = b / (a.b / a.bk);
     const float c = fabsf(a.scale_log2);      // |scale| * log2(e); a negative scale is folded into Q
     const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
@@ -222,7 +214,7 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
             }
         }
     };
-    const int npre = min(ng, AHEAD);
+    const int npre = min(ng, NS - 1);
     for (int blk = 0; blk < npre; ++blk) issue(blk);
 
     // ---- Q: wait for its loads only, round to f16 (ggml's Q conversion, sign
@@ -437,28 +429,34 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     }
 
     // ---- main loop: full blocks 0 .. nf - 2 ------------------------------------
-    // At the start of iteration t block t + 7 goes into slot (t - 1) % 8
-    // (block t - 1 was last read in iteration t - 1, before its barrier); at
-    // its end block t + 2 must have landed (read at the top of iteration t + 1).
-    // Every wavefront passes one barrier per block of the longest group (ni),
-    // plus the prologue's and the merge's.
+    // Copies: blocks 0 .. NS - 2 before the loop; between the halves of
+    // iteration 0 block NS - 1 (its slot is still unused), of iteration
+    // t >= 1 block t + NS into the slot of block t (read in iteration t - 1,
+    // before its barrier); block NS at the top of iteration 1 (block 0 is
+    // read after the prologue's barrier). At the end of iteration t block
+    // t + 2 must have landed (read at the top of iteration t + 1). Every
+    // wavefront passes one barrier per block of the longest group (ni), plus
+    // the prologue's and the merge's.
     for (int t = 0; t + 1 < nf; ++t) {
-        if (t + AHEAD < ng) issue(t + AHEAD);
+        if (t == 1 && NS < ng) issue(NS);
         read_k(t + 1, kr);
-        // H1: S_A(t+1), PV_A(t) on the matrix pipe; softmax of S_B(t). The
+        // H1: PV_A(t), S_A(t+1) on the matrix pipe; softmax of S_B(t). The
         // MFMAs come first in the source so they share a basic block with
         // the softmax's fast path (its rare rescale branch closes the block)
-        // and the scheduler can interleave the two.
-        s_mfma(sa, qa, kr);
+        // and the scheduler can interleave the two; PV_A first, as its
+        // operands are in registers while K_{t+1} lands.
         pv_mfma(oa, pa, vr);
+        s_mfma(sa, qa, kr);
         softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb);
+        if ((t == 0 ? NS - 1 : t + NS) < ng) issue(t == 0 ? NS - 1 : t + NS);
         // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
         pv_mfma(ob, pb, vr);
         read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
         s_mfma(sb, qb, kr);
         softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa);
-        // loads of blocks t + 3 .. min(t + 7, ng - 1) may stay in flight
-        wait_blocks<NLD>(max(min(t + AHEAD, ng - 1) - (t + 2), 0));
+        // blocks issued so far: up to NS - 1 (t = 0), t + NS (t >= 1)
+        const int last = min(t >= 1 ? t + NS : NS - 1, ng - 1);
+        wait_blocks<NLD>(max(last - (t + 2), 0));
         __syncthreads();
     }
     // (no loads are issued from here on)
@@ -495,7 +493,6 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     // published data) writes them normalised to the staging tile, row r at
     // r * 256 bytes with 16-byte chunk j at position j ^ (r & 15); then all
     // wavefronts store full rows.
-    constexpr int PUB = SH::PUB;
     constexpr int EPW = 64 / KVG;                   // elements merged per wavefront
     static_assert(EPW % 4 == 0 && EPW <= 32, "a wavefront's elements lie in one half");
     float* xs = (float*)smem;
@@ -575,33 +572,27 @@ __global__ __launch_bounds__(SH::NT) void fa_prefill64_pp(AttnArgs a, int nqg, i
     }
 }
 
-template <class SH>
-static hipError_t launch_pp_shape(const AttnArgs& a, hipStream_t st) {
+// hd 64 without a mask: 128 query rows x 4 KV groups per workgroup.
+hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
     using namespace pp;
-    const int nqg = (a.nq + SH::BM - 1) / SH::BM;
+    const int nqg = (a.nq + BM - 1) / BM;
     const int nblk = (a.nkv + BK - 1) / BK;
-    const int ni = (nblk + SH::KVG - 1) / SH::KVG;
+    const int ni = (nblk + KVG - 1) / KVG;
     const int64_t nwg = (int64_t)nqg * a.hq * a.b;
     if (nwg <= 0 || nwg > 0x7fffffff || nblk <= 0) return hipErrorInvalidValue;
     // |scale| * log2(e) equal, bit for bit, to the literal in the kernel
     const float c8 = 0.125f * kLog2e;
     const bool is_c8 = fabsf(a.scale_log2) == c8 && __builtin_bit_cast(uint32_t, c8) == 0x3e38aa3bu;
-    const dim3 grid((unsigned)nwg), block(SH::NT);
+    const GridMap gm = GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
+    const dim3 grid((unsigned)nwg), block(NT);
     if (a.q_f16) {
-        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<SH, true, true>), grid, block, 0, st, a, nqg, nblk, ni);
-        else hipLaunchKernelGGL((fa_prefill64_pp<SH, true, false>), grid, block, 0, st, a, nqg, nblk, ni);
+        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<true, true>), grid, block, 0, st, a, gm, nblk, ni);
+        else hipLaunchKernelGGL((fa_prefill64_pp<true, false>), grid, block, 0, st, a, gm, nblk, ni);
     } else {
-        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<SH, false, true>), grid, block, 0, st, a, nqg, nblk, ni);
-        else hipLaunchKernelGGL((fa_prefill64_pp<SH, false, false>), grid, block, 0, st, a, nqg, nblk, ni);
+        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<false, true>), grid, block, 0, st, a, gm, nblk, ni);
+        else hipLaunchKernelGGL((fa_prefill64_pp<false, false>), grid, block, 0, st, a, gm, nblk, ni);
     }
     return hipGetLastError();
-}
-
-// hd 64 without a mask. shape 1: one wavefront per SIMD (128 query rows x 2
-// KV groups); shape 2: two per SIMD (128 query rows x 4 KV groups).
-hipError_t launch_prefill64_pp(const AttnArgs& a, int shape, hipStream_t st) {
-    if (shape == 1) return launch_pp_shape<pp::Shape1>(a, st);
-    return launch_pp_shape<pp::Shape2>(a, st);
 }
 
 }  // namespace vxfa

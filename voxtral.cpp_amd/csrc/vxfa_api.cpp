@@ -27,20 +27,17 @@ constexpr size_t kRecordBytes = (size_t)8 << 20;        // e.g. 256 (batch, kv h
 constexpr size_t kStageBytes = (size_t)32 << 20;        // F32 K and V of 8192 rows x 1024 as f16
 
 // Launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
-// VXFA_PREFILL_WAVES, VXFA_PREFILL_PP, VXFA_PP_SHAPE), read from the
-// environment; 0 = heuristic.
+// VXFA_PREFILL_WAVES, VXFA_PREFILL_PP), read from the environment;
+// 0 = heuristic.
 struct Tuning {
     int split_override = 0;
     int waves_override = 0;
-    // VXFA_PREFILL_PP=0 routes hd 64 unmasked prefill to the general kernel;
-    // VXFA_PP_SHAPE picks its workgroup shape (1 or 2, 0 = default)
+    // VXFA_PREFILL_PP=0 routes hd 64 unmasked prefill to the general kernel
     bool pp_enabled = true;
-    int pp_shape = 0;
     void read_env() {
         if (const char* e = getenv("VXFA_DECODE_SPLIT")) split_override = atoi(e);
         if (const char* e = getenv("VXFA_PREFILL_WAVES")) waves_override = atoi(e);
         if (const char* e = getenv("VXFA_PREFILL_PP")) pp_enabled = atoi(e) != 0;
-        if (const char* e = getenv("VXFA_PP_SHAPE")) pp_shape = atoi(e);
     }
 };
 
@@ -504,7 +501,7 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             // (scale 0 goes to the general kernel: the pipelined one folds the
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel
-            e = vxfa::launch_prefill64_pp(a, w.tune.pp_shape, st);
+            e = vxfa::launch_prefill64_pp(a, st);
         } else {
             // query-row wavefronts per workgroup (each with its KV partner
             // wavefronts): 4 shares every staged K/V step among 128 query rows;
