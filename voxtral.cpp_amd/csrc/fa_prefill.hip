@@ -311,6 +311,25 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     // With a mask tensor the scan's loads go first and Q's follow them at
     // once, so the scan waits for its own loads only.
     if constexpr (MM != 1) issue_q();
+    // With a mask tensor, first one word of every 128-byte line of the step a
+    // causal mask starts with (step 0) is read into registers, so that its
+    // K/V are on their way to L2 while the scan runs and its LDS copies,
+    // issued after the scan, find them there. These are plain loads the
+    // compiler sees (their registers stay theirs until the words are consumed
+    // below); the copies themselves are not issued before the scan.
+    constexpr int WLPR = D / 64;                      // 128-byte lines per K/V row
+    constexpr int WARM = (BS * WLPR + NT - 1) / NT;   // lines per thread per matrix
+    uint32_t warm[MM == 1 ? 2 * WARM : 1];
+    if constexpr (MM == 1) {
+        const int wrows = min(BS, a.nkv);
+#pragma unroll
+        for (int u = 0; u < WARM; ++u) {
+            const int line = min(tid + NT * u, wrows * WLPR - 1);
+            const int64_t wr = line / WLPR;
+            warm[2 * u] = *(const uint32_t*)(kb + wr * a.k_nb1 + (line % WLPR) * 128);
+            warm[2 * u + 1] = *(const uint32_t*)(vb + wr * a.v_nb1 + (line % WLPR) * 128);
+        }
+    }
     // rounds the F32 rows to f16 (ggml's Q conversion), rotating them first
     // when a rotary embedding is given; zeroes rows past n_q
     auto finish_q = [&]() {
@@ -675,6 +694,12 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
         if (MASK && kv0 < a.nkv && tclass(kv0) == 3) load_mask(kv0, mwa);
     }
     finish_q();
+    if constexpr (MM == 1) {   // the words warming step 0 (their wait joins the one below)
+        uint32_t wsum = 0;
+#pragma unroll
+        for (int u = 0; u < 2 * WARM; ++u) wsum ^= warm[u];
+        asm volatile("" ::"v"(wsum));
+    }
     wait_all_mem();
     __syncthreads();
     while (s_cur >= 0) {
