@@ -486,30 +486,30 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     for (int tt = ng; tt < ni; ++tt) __syncthreads();
 
     // ---- merge the KV groups through LDS (the ring is free), normalise ------------
-    // Every wavefront publishes its (O, m, l) element-major (its 64 lanes write
-    // consecutive words). Wavefront (kg, wq) then merges 64 / KVG of the 64
-    // O elements of query tile wq over all groups (all of one half, A or B),
-    // in group order, and after a barrier (the staging tile overlaps the
-    // published data) writes them normalised to the staging tile, row r at
-    // r * 256 bytes with 16-byte chunk j at position j ^ (r & 15); then all
-    // wavefronts store full rows.
+    // Every wavefront publishes its (O, m, l) as 17 chunks of 4 floats per lane,
+    // chunk-major (chunk c of lane l at floats 256 c + 4 l: one 16-byte write
+    // and read per chunk, the 64 lanes' chunks contiguous): chunk c < 16 holds
+    // O elements 4c .. 4c + 3 (element e = 32 x + 16 v + j is accumulator j of
+    // vector v of half x), chunk 16 holds (m_A, m_B, l_A, l_B). Wavefront
+    // (kg, wq) then merges elements [16 kg, 16 kg + 16) of query tile wq over
+    // all groups (one O vector of one half), in group order, and after a
+    // barrier (the staging tile overlaps the published data) writes them
+    // normalised to the staging tile, row r at r * 256 bytes with 16-byte
+    // chunk j at position j ^ (r & 15); then all wavefronts store full rows.
     constexpr int EPW = 64 / KVG;                   // elements merged per wavefront
     static_assert(EPW % 4 == 0 && EPW <= 32, "a wavefront's elements lie in one half");
+    static_assert(PUB == 17 * 4, "published chunks");
     float* xs = (float*)smem;
     char* ost = smem;
     {
-        float* w = xs + (kg * NQT + wq) * PUB * 64 + lane;
+        floatx4* w = (floatx4*)(xs + (kg * NQT + wq) * PUB * 64) + lane;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                w[(db * 16 + j) * 64] = oa[db][j];
-                w[(32 + db * 16 + j) * 64] = ob[db][j];
-            }
-        w[64 * 64] = ma;
-        w[65 * 64] = mb;
-        w[66 * 64] = la;
-        w[67 * 64] = lb;
+        for (int c = 0; c < 16; ++c) {
+            const floatx16& o = (c < 8) ? oa[(c % 8) / 4] : ob[(c % 8) / 4];
+            const int j0 = 4 * (c % 4);
+            w[c * 64] = floatx4{o[j0], o[j0 + 1], o[j0 + 2], o[j0 + 3]};
+        }
+        w[16 * 64] = floatx4{ma, mb, la, lb};
     }
     __syncthreads();
     const int e0 = kg * EPW;        // first element: 0..31 half A, 32..63 half B
@@ -520,9 +520,9 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         float M = -INFINITY;
 #pragma unroll
         for (int g = 0; g < KVG; ++g) {
-            const float* r = xs + (g * NQT + wq) * PUB * 64 + lane;
-            mg[g] = r[(64 + x) * 64];
-            lg[g] = r[(66 + x) * 64];
+            const floatx4 ml = ((const floatx4*)(xs + (g * NQT + wq) * PUB * 64))[16 * 64 + lane];
+            mg[g] = x ? ml[1] : ml[0];
+            lg[g] = x ? ml[3] : ml[2];
             M = fmaxf(M, mg[g]);
         }
         const float Ms = (M == -INFINITY) ? 0.f : M;
@@ -537,14 +537,19 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
 #pragma unroll
         for (int g = 0; g < KVG; ++g) wg[g] *= inv;
+        floatx4 og[KVG][EPW / 4];
+#pragma unroll
+        for (int g = 0; g < KVG; ++g)
+#pragma unroll
+            for (int q = 0; q < EPW / 4; ++q)
+                og[g][q] = ((const floatx4*)(xs + (g * NQT + wq) * PUB * 64))[(e0 / 4 + q) * 64 + lane];
 #pragma unroll
         for (int q = 0; q < EPW / 4; ++q)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float acc = 0.f;
 #pragma unroll
-                for (int g = 0; g < KVG; ++g)
-                    acc = fmaf(wg[g], xs[(g * NQT + wq) * PUB * 64 + (e0 + 4 * q + e) * 64 + lane], acc);
+                for (int g = 0; g < KVG; ++g) acc = fmaf(wg[g], og[g][q][e], acc);
                 res[q][e] = acc;
             }
     }
