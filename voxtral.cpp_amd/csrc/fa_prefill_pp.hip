@@ -107,6 +107,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // every LDS read of this wavefront has returned (s_waitcnt lgkmcnt(0))
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
+// the main loop's wait: at most k blocks' loads in flight, 0 <= k <= 2
+template <int NLD>
+__device__ __forceinline__ void wait_blocks_loop(int k) {
+    constexpr int L = 2 * NLD;
+    if (k >= 2) wait_vmcnt<2 * L>();
+    else if (k == 1) wait_vmcnt<L>();
+    else wait_vmcnt<0>();
+}
+
 // wait until at most k blocks' loads (2 NLD instructions each) are in flight
 template <int NLD>
 __device__ __forceinline__ void wait_blocks(int k) {
@@ -456,7 +465,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa);
         // blocks issued so far: up to NS - 1 (t = 0), t + NS (t >= 1)
         const int last = min(t >= 1 ? t + NS : NS - 1, ng - 1);
-        wait_blocks<NLD>(max(last - (t + 2), 0));
+        wait_blocks_loop<NLD>(last - (t + 2));   // 2 at most: last <= t + NS
         __syncthreads();
     }
     // (no loads are issued from here on)
