@@ -633,7 +633,7 @@ def main():
                    "global_batch": 1, "seq_len": 1500, "heads": 20, "head_dim": 64, "layers": 32},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic(HEADLINE_KERNEL),
-                     "kernel": "fa_prefill64_pp<Shape<2, 4, 4>, false, true>", "us_per_launch": us_layer,
+                     "kernel": "fa_prefill64_pp<false, true>", "us_per_launch": us_layer,
                      "traffic_unit": "bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "algorithmic_bytes": 2 * 1500 * 20 * 64 * 2 + 2 * 1500 * 20 * 64 * 4},
         "cpu_baseline": cpu,
