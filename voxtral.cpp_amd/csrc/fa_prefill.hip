@@ -516,6 +516,14 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
                 }
             }
         } else {
+            // element loads from a clamped position, positions past n_kv
+            // replaced afterwards: a load under a branch makes the compiler
+            // wait for it before issuing the next one
+            uint16_t raw[2][16];
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) raw[kvb][j] = mrow[min(kv0 + 32 * kvb + pf_kv_of(hh, j), a.nkv - 1)];
 #pragma unroll
             for (int kvb = 0; kvb < 2; ++kvb)
 #pragma unroll
@@ -524,7 +532,7 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
 #pragma unroll
                     for (int e = 0; e < 2; ++e) {
                         const int kv = kv0 + 32 * kvb + pf_kv_of(hh, 2 * w + e);
-                        const uint32_t bits = kv < a.nkv ? mrow[kv] : kF16NegInf;
+                        const uint32_t bits = kv < a.nkv ? (uint32_t)raw[kvb][2 * w + e] : kF16NegInf;
                         pair |= bits << (16 * e);
                     }
                     mw[kvb][w] = pair;
