@@ -162,12 +162,14 @@ __device__ __forceinline__ void rope8_tab(float (&x)[8], int d0, const float2* c
     }
 }
 
-__device__ __forceinline__ void rope8(float (&x)[8], int p, int d0, float ts, int n_dims) {
+// dims d0 .. d0 + N - 1 (N = 4 or 8); rope8 = rope_n<8>
+template <int N>
+__device__ __forceinline__ void rope_n(float (&x)[N], int p, int d0, float ts, int n_dims) {
     if (d0 >= n_dims) return;
     float th = (float)p;
     for (int j = 0; j < d0 / 2; ++j) th *= ts;   // the running product up to pair d0 / 2
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < N / 2; ++k) {
         if (d0 + 2 * k < n_dims) {
             // angles reach n_ctx radians: reduce by 2 pi in double first (error
             // ~1e-12), then sincosf's short-argument path applies
@@ -182,6 +184,10 @@ __device__ __forceinline__ void rope8(float (&x)[8], int p, int d0, float ts, in
         }
         th *= ts;
     }
+}
+
+__device__ __forceinline__ void rope8(float (&x)[8], int p, int d0, float ts, int n_dims) {
+    rope_n<8>(x, p, d0, ts, n_dims);
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -383,6 +389,9 @@ constexpr int kDecodeWaves = 4;      // wavefronts per decode workgroup
 constexpr int dec_record_floats(int D, int G) { return G * D + ((2 * G + 3) & ~3); }
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
 hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t stream);
+// masked hd 128 prefill with n_kv <= 512 (a mask tensor or an implicit mask;
+// a rotary embedding of F32 Q)
+hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
 // F32 -> f16 copy of a [D, n, H, B] view (byte strides nb1..nb3, rows

@@ -1,0 +1,562 @@
+// fa_prefill_pair.hip — short masked prefill for gfx950: hd 128, n_kv <= 512,
+// 32-row query tiles paired from both ends of the sequence.
+//
+// Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for voxtral.cpp's
+// decoder prefill: GQA 32/8, hd 128, causal mask (src/voxtral.cpp:1802; mask
+// filled by fill_causal_mask :2104-2111 and cast at :1801), or the same call
+// with the mask given as a formula (vxfa_flash_attn_ext_implicit).
+//
+// Why a kernel of its own: at this size the work is a few microseconds of
+// matrix time spread over 224 workgroups, and a kernel that walks the KV axis
+// in steps pays a memory round trip per step on its longest walk. Here every
+// wavefront computes (about) one block, and all of a workgroup's loads are in
+// flight at once.
+//
+// Work decomposition
+//   A head's query rows form nt = ceil(n_q / 32) tiles. Workgroup p of a head
+//   takes tiles A = p and B = nt - 1 - p (B alone when they meet). Under a
+//   causal mask tile i meets floor(i / 2) + 1 live 64-position KV tiles, so
+//   every pair holds about the same number of live (tile, KV tile) blocks:
+//   8 at n_q = 439, one per wavefront.
+//   Block classes: dead (skipped), all-zero mask (computed without the mask)
+//   or mixed (mask values added). With an implicit mask they follow from the
+//   formula; with a mask tensor each wavefront first reads the mask of two
+//   candidate blocks, (B, w) and (A, 7 - w), and classifies them.
+//   Assignment: B's live blocks go to wavefronts 0 .. wB - 1, A's to the rest
+//   in reverse order (wB in proportion to the live counts), so under a causal
+//   mask each wavefront computes the block it classified, whose mask values
+//   are already in its registers. A wavefront with several blocks walks them
+//   with the online softmax.
+//   Merge: every wavefront publishes (O, m, l) to LDS; the wavefronts of a
+//   tile then each merge and store a quarter (or so) of its elements.
+// Memory: every live V tile of the pair goes to LDS once (direct
+//   global-to-LDS copies, 16 KiB per tile, at most 8), shared by both tiles'
+//   wavefronts; K rows go straight from global memory into the MFMA operand
+//   registers of the wavefront that uses them; Q of both tiles is rotated
+//   (vxfa_flash_attn_ext_rope: ggml's rope mode 0 at each row's position),
+//   rounded to f16 (ggml's Q conversion) and staged in LDS.
+// MFMA layouts, the row-to-KV permutation within a 32-position block, the V
+//   tile's XOR swizzle and the transposed V^T reads are those of
+//   fa_prefill.hip (v_mfma_f32_32x32x16_f16: S^T = K Q^T, O^T = V^T P^T).
+#include "fa_common.h"
+
+#include <type_traits>
+
+namespace vxfa {
+
+namespace pr {
+constexpr int D = 128;
+constexpr int KS = D / 16;       // S-MFMA k-steps
+constexpr int DB = D / 32;       // O^T row blocks
+constexpr int TK = 64;           // KV positions per KV tile
+constexpr int MAXK = 8;          // KV tiles in LDS: n_kv <= 512
+constexpr int NW = 8;            // wavefronts
+constexpr int NT = 64 * NW;
+constexpr int ROW = D * 2;       // bytes per f16 row
+constexpr int VT = TK * ROW;     // one V tile (16 KiB)
+constexpr int QT = 32 * ROW;     // one staged query tile (8 KiB)
+constexpr int NE = 16 * DB;      // O elements per lane
+}  // namespace pr
+
+// A barrier that orders LDS accesses only (a full __syncthreads() would also
+// wait for every global load still in flight).
+__device__ __forceinline__ void pr_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int MM, bool QF16>   // MM 1: mask tensor, 2: implicit mask
+__global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm, int nt, int nk) {
+    using namespace pr;
+    static_assert(MM == 1 || MM == 2, "masked calls only");
+    __shared__ __attribute__((aligned(16))) char sV[MAXK * VT];   // V tiles; then the published O
+    __shared__ __attribute__((aligned(16))) char sQ[2 * QT];      // query tiles A (slot 0), B (slot 1)
+    __shared__ float s_ml[2 * NW * 64];                           // published m, then l
+    __shared__ uint8_t s_cls[2 * MAXK];                           // classes of (A, j), then (B, j)
+    static_assert(NW * NE * 64 * 4 <= MAXK * VT, "published O fits the V area");
+
+    int p, h, b, hk, bkv;
+    gm.locate(blockIdx.x, p, h, b, hk, bkv);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nl = lane & 31;
+    const int hh = lane >> 5;
+    const int tA = p, tB = nt - 1 - p;
+    const bool hasA = tA < tB;
+    const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
+    const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
+    const float c = a.scale_log2;
+
+    // ---- mask words of block (T, j) for this lane ----------------------------
+    // Row 32 T + nl; element 2 w + e of 32-block kvb is half e of mw[kvb][w].
+    // Lane half 0 holds positions 0..15 of each 32-block in order, half 1
+    // positions 16..31 with its two 8-position halves swapped (the row-to-KV
+    // permutation). Positions past n_kv and rows past n_q read -inf.
+    const char* mplane = nullptr;
+    if constexpr (MM == 1)
+        mplane = (const char*)a.mask + (int64_t)(h % a.hm) * a.m_nb2 + (int64_t)(b % a.bm) * a.m_nb3;
+    // Tensor: the lane's 16 entries of a 32-block are 32 bytes at any 2-byte
+    // alignment (voxtral's n x n rows are 2n bytes apart), read as the three
+    // 16-byte-aligned chunks that cover them. A chunk past the row's last data
+    // granule is replaced by that granule, so every chunk read holds mask data
+    // of the row (same allocation, same page); entries taken from it lie past
+    // n_kv and are replaced by -inf.
+    auto mw_issue = [&](int T, int j, u32x4 (&ch)[2][3]) {
+        const int row = 32 * T + nl;
+        const char* rowp = mplane + (int64_t)(row < a.nq ? row : 0) * a.m_nb1;
+        const uintptr_t last = (reinterpret_cast<uintptr_t>(rowp) + 2 * (uintptr_t)a.nkv - 1) & ~(uintptr_t)15;
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb) {
+            const char* seg = rowp + 2 * (TK * j + 32 * kvb + 16 * hh);
+            const int sh = (int)(reinterpret_cast<uintptr_t>(seg) & 15);
+            const char* pa = seg - sh;
+            const int lim = (int)((intptr_t)last - (intptr_t)reinterpret_cast<uintptr_t>(pa));   // multiple of 16
+#pragma unroll
+            for (int i = 0; i < 3; ++i) ch[kvb][i] = *(const u32x4*)(pa + min(16 * i, lim));
+        }
+    };
+    auto mw_finish = [&](int T, int j, const u32x4 (&ch)[2][3], uint32_t (&mw)[2][8]) {
+        const int row = 32 * T + nl;
+        const char* rowp = mplane + (int64_t)(row < a.nq ? row : 0) * a.m_nb1;
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb) {
+            const int sh = (int)(reinterpret_cast<uintptr_t>(rowp + 2 * (TK * j + 32 * kvb + 16 * hh)) & 15);
+            const int q4 = sh >> 2, s2 = sh & 2;
+            uint32_t d[12];
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) d[4 * i + k] = ch[kvb][i][k];
+            uint32_t e[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) e[k] = q4 == 0 ? d[k] : q4 == 1 ? d[k + 1] : q4 == 2 ? d[k + 2] : d[k + 3];
+            uint32_t wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) wv[k] = __builtin_amdgcn_alignbyte(e[k + 1], e[k], (uint32_t)s2);
+#pragma unroll
+            for (int w = 0; w < 8; ++w) mw[kvb][w] = hh ? wv[(w + 4) & 7] : wv[w];
+        }
+        if (row >= a.nq) {
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                for (int w = 0; w < 8; ++w) mw[kvb][w] = 0xFC00FC00u;
+        } else if (TK * j + TK > a.nkv) {
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                for (int w = 0; w < 8; ++w)
+#pragma unroll
+                    for (int e2 = 0; e2 < 2; ++e2)
+                        if (TK * j + 32 * kvb + pf_kv_of(hh, 2 * w + e2) >= a.nkv)
+                            mw[kvb][w] = (mw[kvb][w] & (0xFFFF0000u >> (16 * e2))) | (0xFC00u << (16 * e2));
+        }
+    };
+    // Implicit: 0 where row attends kv, -inf elsewhere (rows past n_q use row
+    // 0, as the tensor path of fa_prefill.hip does; they are never stored).
+    auto mw_formula = [&](int T, int j, uint32_t (&mw)[2][8]) {
+        const int row = 32 * T + nl;
+        const int64_t lastc = (int64_t)(row < a.nq ? row : 0) + a.im_offset;
+        const int64_t firstc = a.im_window > 0 ? lastc - a.im_window + 1 : INT64_MIN;
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                uint32_t pair = 0;
+#pragma unroll
+                for (int e2 = 0; e2 < 2; ++e2) {
+                    const int kv = TK * j + 32 * kvb + pf_kv_of(hh, 2 * w + e2);
+                    const bool live = kv < a.nkv && (int64_t)kv <= lastc && (int64_t)kv >= firstc;
+                    pair |= (live ? 0u : (uint32_t)kF16NegInf) << (16 * e2);
+                }
+                mw[kvb][w] = pair;
+            }
+    };
+    // class of block (T, j) from the formula: 0 dead, 1 every entry 0, 3 mixed
+    // (a KV tile running past n_kv is mixed)
+    auto cls_formula = [&](int T, int j) -> int {
+        const int64_t r0 = 32 * T, r1 = (int64_t)min(32 * T + 32, a.nq) - 1;
+        const int64_t c0 = TK * j, c1 = (int64_t)min(TK * j + TK, a.nkv) - 1;
+        if (r1 < r0 || c1 < c0) return 0;
+        const int64_t off = a.im_offset, W = a.im_window;
+        if (c0 > r1 + off || (W > 0 && c1 < r0 + off - W + 1)) return 0;
+        const bool all = c1 <= r0 + off && (W == 0 || c0 >= r1 + off - W + 1);
+        return (all && TK * j + TK <= a.nkv) ? 1 : 3;
+    };
+
+    // ---- Q loads of both tiles (rows past n_q load row n_q - 1, zeroed when
+    // staged; no load sits under a branch) ---------------------------------------
+    constexpr int QCH = QF16 ? 16 : 32;           // 16-byte global chunks per row
+    constexpr int QPT = 2 * 32 * QCH / NT;        // per thread
+    floatx4 qraw[QPT];
+    int qpos[QPT];   // rotary position of the chunk's row (F32 Q)
+    auto issue_q = [&]() {
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+            const int i = tid + NT * u;
+            const int s = i / (32 * QCH), r = (i / QCH) % 32, cch = i % QCH;
+            const int row = min(32 * (s ? tB : tA) + r, a.nq - 1);
+            qraw[u] = *(const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 + (int64_t)h * a.q_nb2 +
+                                        (int64_t)b * a.q_nb3 + cch * 16);
+            if constexpr (!QF16) {
+                // read without a branch: without a rotary embedding it reads
+                // the first word of Q, unused
+                const int* pp = a.rope_pos ? a.rope_pos + ((int64_t)b * a.nq + row) : (const int*)a.q;
+                qpos[u] = *pp;
+            }
+        }
+    };
+
+    // ---- classes of the pair's blocks ------------------------------------------
+    // candidates of this wavefront (mask tensor): (B, wave) and (A, 7 - wave)
+    const int jB = wave, jA = MAXK - 1 - wave;
+    const bool candB = jB < nk, candA = hasA && jA < nk;
+    uint32_t mwB[2][8], mwA[2][8];
+    uint32_t liveA = 0, liveB = 0, mixA = 0, mixB = 0;
+    if constexpr (MM == 1) {
+        u32x4 chB[2][3], chA[2][3];
+        // (a candidate that does not exist reads tile B's or A's first block)
+        mw_issue(tB, candB ? jB : 0, chB);
+        mw_issue(tA, candA ? jA : 0, chA);
+        issue_q();   // after the mask loads: their wait does not include Q's
+        mw_finish(tB, candB ? jB : 0, chB, mwB);
+        mw_finish(tA, candA ? jA : 0, chA, mwA);
+        auto classify = [&](const uint32_t (&mw)[2][8]) -> int {
+            bool live = false, nonzero = false;
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                for (int w = 0; w < 8; ++w) {
+                    live |= mw[kvb][w] != 0xFC00FC00u;
+                    nonzero |= (mw[kvb][w] & 0x7FFF7FFFu) != 0u;
+                }
+            return !__any(live) ? 0 : __any(nonzero) ? 3 : 1;
+        };
+        const int cB = classify(mwB), cA = classify(mwA);
+        if (lane == 0) {
+            if (candB) s_cls[MAXK + jB] = (uint8_t)cB;
+            if (candA) s_cls[jA] = (uint8_t)cA;
+        }
+        pr_lds_barrier();
+        for (int j = 0; j < nk; ++j) {
+            const int kB = s_cls[MAXK + j];
+            liveB |= (kB != 0 ? 1u : 0u) << j;
+            mixB |= (kB == 3 ? 1u : 0u) << j;
+            if (hasA) {
+                const int kA = s_cls[j];
+                liveA |= (kA != 0 ? 1u : 0u) << j;
+                mixA |= (kA == 3 ? 1u : 0u) << j;
+            }
+        }
+    } else {
+        issue_q();
+        for (int j = 0; j < nk; ++j) {
+            const int kB = cls_formula(tB, j);
+            liveB |= (kB != 0 ? 1u : 0u) << j;
+            mixB |= (kB == 3 ? 1u : 0u) << j;
+            if (hasA) {
+                const int kA = cls_formula(tA, j);
+                liveA |= (kA != 0 ? 1u : 0u) << j;
+                mixA |= (kA == 3 ? 1u : 0u) << j;
+            }
+        }
+    }
+    liveA = __builtin_amdgcn_readfirstlane(liveA);
+    liveB = __builtin_amdgcn_readfirstlane(liveB);
+    mixA = __builtin_amdgcn_readfirstlane(mixA);
+    mixB = __builtin_amdgcn_readfirstlane(mixB);
+
+    // ---- assignment ------------------------------------------------------------
+    const int nA = __builtin_popcount(liveA), nB = __builtin_popcount(liveB);
+    int wB = NW;
+    if (hasA) {
+        if (nA + nB == 0) wB = NW / 2;
+        else wB = min(max((NW * nB + (nA + nB) / 2) / (nA + nB), 1), NW - 1);
+    }
+    const bool onB = wave < wB;
+    const int T = onB ? tB : tA;
+    const int wT = onB ? wB : NW - wB;             // wavefronts of this tile
+    const int iT = onB ? wave : NW - 1 - wave;     // index among them
+    const uint32_t live = onB ? liveB : liveA;
+    const uint32_t mix = onB ? mixB : mixA;
+    const int nT = onB ? nB : nA;
+    const int nblk = nT > iT ? (nT - iT + wT - 1) / wT : 0;
+    // KV tile of this wavefront's k-th block: the (iT + k wT)-th live tile
+    auto block_tile = [&](int k) -> int {
+        int r = iT + k * wT;
+        for (int j = 0; j < nk; ++j)
+            if ((live >> j) & 1u) {
+                if (r == 0) return j;
+                --r;
+            }
+        return 0;
+    };
+
+    // ---- K of the first block: A-operand rows straight from global memory ----
+    // (row nl of 32-block kvb is K row krow of it; chunk 2 ks + hh)
+    const int krow = [&] {
+        const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
+        return ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
+    }();
+    half8 kr[2][KS];
+    auto issue_k = [&](int j) {
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb) {
+            const int kv = min(TK * j + 32 * kvb + krow, a.nkv - 1);
+            const char* kp = kb + (int64_t)kv * a.k_nb1 + hh * 16;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) kr[kvb][ks] = *(const half8*)(kp + ks * 32);
+        }
+    };
+    // mask words of the first block: the classification's when it is one of
+    // this wavefront's candidates, else read again (finished after the wait
+    // below, so the V copies are not held back by them)
+    uint32_t mw[2][8];
+    u32x4 chr[2][3];
+    bool reload = false;
+    int j0 = 0;
+    if (nblk > 0) {
+        j0 = block_tile(0);
+        issue_k(j0);
+        if ((mix >> j0) & 1u) {
+            if constexpr (MM == 1) {
+                if (onB && j0 == jB) {
+#pragma unroll
+                    for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                        for (int w = 0; w < 8; ++w) mw[kvb][w] = mwB[kvb][w];
+                } else if (!onB && j0 == jA) {
+#pragma unroll
+                    for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+                        for (int w = 0; w < 8; ++w) mw[kvb][w] = mwA[kvb][w];
+                } else {
+                    mw_issue(T, j0, chr);
+                    reload = true;
+                }
+            } else {
+                mw_formula(T, j0, mw);
+            }
+        }
+    }
+
+    // ---- V: every live KV tile of the pair into LDS, once ---------------------
+    // Tile j's rows 4 g .. 4 g + 3 (g = 0..15) are one copy instruction;
+    // wavefront w issues g = w and w + 8 of every tile. Lane l writes LDS
+    // chunk l % 16 of row 4 g + l / 16, which holds the row's chunk
+    // (l % 16) ^ swizzle(row). Rows past n_kv repeat row n_kv - 1.
+    const uint32_t used = liveA | liveB;
+    {
+        const uint32_t lds_v = lds_offset(sV);
+        const int rl = lane >> 4;
+        const int col = ((lane & 15) ^ swz_v<D>(rl)) * 16;   // swizzle depends on row % 4 = rl
+        for (int j = 0; j < nk; ++j) {
+            if (!((used >> j) & 1u)) continue;
+            const int kv0 = TK * j;
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) {
+                const int g = wave + NW * gg;
+                const int r = 4 * g + rl;
+                const uint32_t dst = lds_v + j * VT + 4 * g * ROW;
+                if (kv0 + TK <= a.nkv) {
+                    dma16(vb + (int64_t)kv0 * a.v_nb1, (uint32_t)r * (uint32_t)a.v_nb1 + col, dst);
+                } else {
+                    const int kv = min(kv0 + r, a.nkv - 1);
+                    dma16_addr(vb + (int64_t)kv * a.v_nb1 + col, dst);
+                }
+            }
+        }
+    }
+
+    // ---- Q: wait for every load, round to f16, stage -------------------------
+    wait_all_mem();
+    if constexpr (MM == 1)
+        if (reload) mw_finish(T, j0, chr, mw);
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int i = tid + NT * u;
+        const int s = i / (32 * QCH), r = (i / QCH) % 32, cch = i % QCH;
+        floatx4 x = qraw[u];
+        if (32 * (s ? tB : tA) + r >= a.nq) x = floatx4{0.f, 0.f, 0.f, 0.f};
+        char* qrow = sQ + s * QT + r * ROW;
+        if constexpr (QF16) {
+            *(floatx4*)(qrow + ((cch ^ (r & 15)) * 16)) = x;
+        } else {
+            // rotated first when a rotary embedding is given (ggml rotates
+            // Q before the attention node)
+            float xr[4] = {x[0], x[1], x[2], x[3]};
+            if (a.rope_pos) rope_n<4>(xr, qpos[u], 4 * cch, a.rope_ts, a.rope_dims);
+            half4 v;
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) v[e2] = (_Float16)xr[e2];
+            *(half4*)(qrow + (((cch >> 1) ^ (r & 15)) * 16) + (cch & 1) * 8) = v;
+        }
+    }
+    __syncthreads();   // Q staged, V tiles visible
+
+    // ---- blocks ----------------------------------------------------------------
+    floatx16 o[DB];
+    float m_run = -INFINITY, l_run = 0.f;
+    const int vq = (lane & 15) >> 2;
+    const int clo = 2 * ((lane & 31) >> 4) + ((lane & 3) >> 1);
+    int vaddr[2][DB];
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+            vaddr[cc][db] = ((hh ? 24 - 8 * cc : 8 * cc) + vq) * ROW + ((4 * db + clo) ^ swz_v<D>(vq)) * 16 +
+                            (lane & 1) * 8;
+    const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    const char* qs = sQ + (onB ? QT : 0) + nl * ROW;
+    // One block at KV tile j. FIRST: O starts at zero (the first PV MFMAs take
+    // a zero accumulator) and no rescale; O is not live before them. The Q
+    // operand of each k-step is read from LDS right before its two MFMAs.
+    auto run_block = [&](auto first_tag, int j, bool mixed) {
+        constexpr bool FIRST = decltype(first_tag)::value;
+        floatx16 S[2];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 qk = *(const half8*)(qs + (((2 * ks + hh) ^ (nl & 15)) * 16));
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb)
+                S[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[kvb][ks], qk, ks == 0 ? floatx16{} : S[kvb], 0, 0, 0);
+        }
+        // scores in log2 units, the mask added (-inf stays -inf)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) {
+                float x = S[kvb][jj] * c;
+                if (mixed) {
+                    const half2 m2 = __builtin_bit_cast(half2, mw[kvb][jj >> 1]);
+                    x = fmaf((float)m2[jj & 1], kLog2e, x);
+                }
+                S[kvb][jj] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = pair32_max(mx);
+        const float mnew = fmaxf(m_run, mx);
+        const float ms = (mnew == -INFINITY) ? 0.f : mnew;
+        if constexpr (!FIRST) {
+            const float alpha = exp2_fast(m_run - ms);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int jj = 0; jj < 16; ++jj) o[db][jj] *= alpha;
+            l_run *= alpha;
+        }
+        m_run = mnew;
+        const char* vt = sV + j * VT;
+        float ls[2] = {0.f, 0.f};
+#pragma unroll
+        for (int pc = 0; pc < 4; ++pc) {
+            const int kvb = pc >> 1, cc = pc & 1;
+            half8 pb;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pb[i] = (_Float16)exp2_fast(S[kvb][8 * cc + i] - ms);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const half2 p2 = {pb[2 * i], pb[2 * i + 1]};
+                ls[i & 1] = __builtin_amdgcn_fdot2(p2, ones, ls[i & 1], false);
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const char* vp = vt + vaddr[cc][db] + 32 * kvb * ROW;
+                const half4 lo4 = lds_read_tr16(vp);
+                const half4 hi4 = lds_read_tr16(vp + 4 * ROW);
+                const half8 va = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, (FIRST && pc == 0) ? floatx16{} : o[db], 0,
+                                                               0, 0);
+            }
+        }
+        l_run += ls[0] + ls[1];
+    };
+    if (nblk > 0) {
+        run_block(std::true_type{}, j0, ((mix >> j0) & 1u) != 0);
+        for (int k = 1; k < nblk; ++k) {
+            const int j = block_tile(k);
+            const bool mixed = ((mix >> j) & 1u) != 0;
+            issue_k(j);
+            if (mixed) {
+                if constexpr (MM == 1) {
+                    u32x4 ch[2][3];
+                    mw_issue(T, j, ch);
+                    mw_finish(T, j, ch, mw);
+                } else {
+                    mw_formula(T, j, mw);
+                }
+            }
+            run_block(std::false_type{}, j, mixed);
+        }
+    } else {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] = floatx16{};
+    }
+
+    // ---- merge each tile over its wavefronts, normalise, store ---------------
+    __syncthreads();   // every V read done: the V area takes the published O
+    {
+        float* pub = (float*)sV + wave * (NE * 64);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) pub[(16 * db + jj) * 64 + lane] = o[db][jj];
+        s_ml[wave * 64 + lane] = m_run;
+        s_ml[NW * 64 + wave * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    // the tile's wavefronts: B's are 0 .. wB - 1, A's wB .. NW - 1
+    const int g0 = onB ? 0 : wB;
+    float M = -INFINITY;
+    for (int g = g0; g < g0 + wT; ++g) M = fmaxf(M, s_ml[g * 64 + lane]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float lsum = 0.f;
+    for (int g = g0; g < g0 + wT; ++g) lsum = fmaf(exp2_fast(s_ml[g * 64 + lane] - Ms), s_ml[NW * 64 + g * 64 + lane], lsum);
+    const float lt = pair32_sum(lsum);
+    const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
+    const int row = 32 * T + nl;
+    // 16 groups of 4 elements (O^T block db, accumulator quad a4: dims
+    // 32 db + 8 a4 + 4 hh .. + 3); this wavefront takes groups iT, iT + wT, ...
+    for (int q = iT; q < 16; q += wT) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int g = g0; g < g0 + wT; ++g) {
+            const float wg = exp2_fast(s_ml[g * 64 + lane] - Ms) * inv;
+            const float* src = (const float*)sV + g * (NE * 64) + (4 * q) * 64 + lane;
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) acc[e2] = fmaf(wg, src[e2 * 64], acc[e2]);
+        }
+        if (row < a.nq) {
+            const int db = q >> 2, a4 = q & 3;
+            float* out = a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 32 * db + 8 * a4 + 4 * hh;
+            *(floatx4*)out = acc;
+        }
+    }
+}
+
+// Short masked prefill: hd 128, a mask tensor or an implicit mask, n_kv <= 512
+// (a rotary embedding of F32 Q applied as it is staged).
+hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t st) {
+    using namespace pr;
+    if (!(a.mask != nullptr || a.im_causal) || (a.rope_pos != nullptr && a.q_f16)) return hipErrorInvalidValue;
+    const int nt = (a.nq + 31) / 32;
+    const int nk = (a.nkv + TK - 1) / TK;
+    if (nt <= 0 || nk <= 0 || nk > MAXK) return hipErrorInvalidValue;
+    const int np = (nt + 1) / 2;
+    const int64_t nwg = (int64_t)np * a.hq * a.b;
+    if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
+    const GridMap gm = GridMap::make((int)nwg, np, a.hq, a.hkv, a.b, a.bk);
+    const dim3 grid((unsigned)nwg), block(NT);
+    if (a.im_causal) {
+        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<2, true>), grid, block, 0, st, a, gm, nt, nk);
+        else hipLaunchKernelGGL((fa_prefill_pair<2, false>), grid, block, 0, st, a, gm, nt, nk);
+    } else {
+        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<1, true>), grid, block, 0, st, a, gm, nt, nk);
+        else hipLaunchKernelGGL((fa_prefill_pair<1, false>), grid, block, 0, st, a, gm, nt, nk);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace vxfa

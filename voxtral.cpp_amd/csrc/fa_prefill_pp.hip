@@ -513,10 +513,10 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     {
         floatx4* w = (floatx4*)(xs + (kg * NQT + wq) * PUB * 64) + lane;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const floatx16& o = (c < 8) ? oa[(c % 8) / 4] : ob[(c % 8) / 4];
-            const int j0 = 4 * (c % 4);
-            w[c * 64] = floatx4{o[j0], o[j0 + 1], o[j0 + 2], o[j0 + 3]};
+        for (int ci = 0; ci < 16; ++ci) {
+            const floatx16& o = (ci < 8) ? oa[(ci % 8) / 4] : ob[(ci % 8) / 4];
+            const int j0 = 4 * (ci % 4);
+            w[ci * 64] = floatx4{o[j0], o[j0 + 1], o[j0 + 2], o[j0 + 3]};
         }
         w[16 * 64] = floatx4{ma, mb, la, lb};
     }

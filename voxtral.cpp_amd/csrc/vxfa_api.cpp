@@ -34,10 +34,13 @@ struct Tuning {
     int waves_override = 0;
     // VXFA_PREFILL_PP=0 routes hd 64 unmasked prefill to the general kernel
     bool pp_enabled = true;
+    // VXFA_PREFILL_PAIR=0 routes short masked hd 128 prefill to the general kernel
+    bool pair_enabled = true;
     void read_env() {
         if (const char* e = getenv("VXFA_DECODE_SPLIT")) split_override = atoi(e);
         if (const char* e = getenv("VXFA_PREFILL_WAVES")) waves_override = atoi(e);
         if (const char* e = getenv("VXFA_PREFILL_PP")) pp_enabled = atoi(e) != 0;
+        if (const char* e = getenv("VXFA_PREFILL_PAIR")) pair_enabled = atoi(e) != 0;
     }
 };
 
@@ -502,6 +505,10 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel
             e = vxfa::launch_prefill64_pp(a, st);
+        } else if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled) {
+            // short masked prefill (voxtral's decoder prefill): paired query
+            // tiles, every live block on its own wavefront
+            e = vxfa::launch_prefill_pair(a, st);
         } else {
             // query-row wavefronts per workgroup (each with its KV partner
             // wavefronts): 4 shares every staged K/V step among 128 query rows;
