@@ -4,17 +4,15 @@ prefill kernel (voxtral.cpp_amd/csrc/fa_prefill_pair.hip).
 For a given shape, stride set and mask it shows, lane by lane, that
 
   * every Q load reads 16 bytes inside an existing query row,
-  * every K load reads 16 bytes inside an existing K row (rows past n_kv
-    clamped),
   * every mask chunk read is a 16-byte-aligned granule holding at least one
     byte of its mask row (rows past n_q read row 0), and the words extracted
     from the three chunks (funnel shift by the row's misalignment, lane half
     1's halves swapped, -inf past n_kv and for rows past n_q) equal the mask
     entries at the positions the accumulator layout assigns to the lane,
-  * every global -> LDS copy of a V tile reads 16 bytes inside an existing V
-    row and lands inside the V area, every byte of a used V tile is written
-    exactly once, and every transposed V^T read of a computed block reads
-    bytes its tile's copies wrote,
+  * every global -> LDS copy of a K or V tile reads 16 bytes inside an
+    existing row (rows past n_kv clamped) and lands inside the LDS area, every
+    byte of a used tile is written exactly once, and every K operand read and
+    transposed V^T read of a computed block finds the global chunk it needs,
   * the assignment computes every live (query tile, KV tile) block exactly
     once and no dead one, and the merge stores every output element of every
     valid query row exactly once.
@@ -51,6 +49,11 @@ def pf_kv_of(hh, j):
 
 def swz_v(r):
     return (np.asarray(r) & 3) << 2
+
+
+def swz_k(r):
+    r = np.asarray(r)
+    return ((r >> 1) ^ (r << 2)) & 15
 
 
 @dataclass
@@ -196,10 +199,59 @@ def mask_words_kernel(sh: Shape, buf, plane_off, T, j, plant=None):
     return out
 
 
+def classify_kernel(sh: Shape, buf, plane_off, T, j, plant=None):
+    """The kernel's cls_issue + cls_eval: each candidate row's 128-byte
+    segment read as 16-byte-aligned chunks, nine lanes per row, seven rows per
+    load, five loads; checks every chunk address, returns the class."""
+    live = nonzero = False
+    for u in range(5):
+        for lane in range(64):
+            lr, lc = lane // 9, lane % 9
+            row = 32 * T + 7 * u + lr
+            ok = lr < 7 and 7 * u + lr < 32 and row < sh.nq
+            rowp = plane_off + (row if ok else 0) * sh.m_nb1
+            last = (rowp + 2 * sh.nkv - 1) & ~15
+            seg = rowp + 2 * TK * j
+            pa = seg - (seg & 15)
+            lim = last - pa
+            a = pa + (16 * lc if plant == "no_chunk_clamp" else min(16 * lc, lim))
+            _check(a % 16 == 0, "classification chunk not 16-byte aligned")
+            _check(a < rowp + 2 * sh.nkv and a + 16 > rowp,
+                   f"classification chunk {a} outside row data [{rowp}, {rowp + 2 * sh.nkv})")
+            c = np.zeros(16, dtype=np.uint8)
+            n = max(0, min(16, len(buf) - a))
+            c[:n] = buf[a:a + n]
+            w16 = c.view(np.uint16)
+            e0 = (pa + 16 * lc - rowp) // 2
+            lo, hi = max(TK * j - e0, 0), min(min(TK * j + TK, sh.nkv) - e0, 8)
+            if not ok or hi <= lo:
+                continue
+            for k in range(lo, hi):
+                v = int(w16[k])
+                live |= v != NEG_INF
+                nonzero |= (v & 0x7FFF) != 0
+    if not live:
+        return 0
+    return 3 if (nonzero or TK * j + TK > sh.nkv) else 1
+
+
 def classify(words):
     live = np.any(words != 0xFC00FC00)
     nonzero = np.any((words & 0x7FFF7FFF) != 0)
     return 0 if not live else (3 if nonzero else 1)
+
+
+def blocks_per_wave(nA, nB, hasA):
+    """Largest number of blocks any wavefront of the pair computes."""
+    wB = assignment(nA, nB, hasA)
+    worst = 0
+    for w in range(NW):
+        onB = w < wB
+        wT = wB if onB else NW - wB
+        iT = w if onB else NW - 1 - w
+        nT = nB if onB else nA
+        worst = max(worst, (nT - iT + wT - 1) // wT if nT > iT else 0)
+    return worst
 
 
 def assignment(nA, nB, hasA, plant=None):
@@ -260,29 +312,23 @@ def _emulate_wg(sh, p, h, bb, hk, bkv, nt, nk, buf, stored, plant):
     # classes
     cls = {}
     if sh.mode == "tensor":
-        ent = lambda row, pos: sh.mask[bb % sh.bm, h % sh.hm, row, pos]
         for w in range(NW):
             jB, jA = w, MAXK - 1 - w
             candB, candA = jB < nk, hasA and jA < nk
-            wb = mask_words_kernel(sh, buf, plane_off, tB, jB if candB else 0, plant)
-            wa = mask_words_kernel(sh, buf, plane_off, tA, jA if candA else 0, plant)
+            cB = classify_kernel(sh, buf, plane_off, tB, jB if candB else 0, plant)
+            cA = classify_kernel(sh, buf, plane_off, tA, jA if candA else 0, plant)
             if candB:
-                exp = mask_words_expected(sh, ent, tB, jB)
-                _check(wb == exp, f"mask words of block ({tB}, {jB}) differ from the entries")
-                cls[(1, jB)] = classify(wb)
+                cls[(1, jB)] = cB
             if candA:
-                exp = mask_words_expected(sh, ent, tA, jA)
-                _check(wa == exp, f"mask words of block ({tA}, {jA}) differ from the entries")
-                cls[(0, jA)] = classify(wa)
+                cls[(0, jA)] = cA
         # the kernel's classes equal the ones the entries give
-        for (s, j), c in cls.items():
-            T = tB if s else tA
+        for (s_, j), c in cls.items():
+            T = tB if s_ else tA
             rows = range(32 * T, min(32 * T + 32, sh.nq))
             vals = [int(sh.mask[bb % sh.bm, h % sh.hm, r, k]) for r in rows for k in range(TK * j, TK * j + TK)
                     if k < sh.nkv]
-            partial = TK * j + TK > sh.nkv or len(rows) < 32
             live = any(v != NEG_INF for v in vals)
-            zero = all(v in (0, 0x8000) for v in vals) and not partial
+            zero = all(v in (0, 0x8000) for v in vals) and TK * j + TK <= sh.nkv
             want = 0 if not live else (1 if zero else 3)
             _check(c == want, f"class of ({T}, {j}): {c}, entries give {want}")
     else:
@@ -309,71 +355,94 @@ def _emulate_wg(sh, p, h, bb, hk, bkv, nt, nk, buf, stored, plant):
             j = live[iT + k * wT]
             key = (T, j)
             computed[key] = computed.get(key, 0) + 1
-            # K loads of the block
-            am, ahb, ab = (LANES & 31) >> 3, ((LANES & 31) >> 2) & 1, LANES & 3
-            krow = np.where(ahb != 0, 16 + ((am + 2) & 3) * 4 + ab, 4 * am + ab)
-            hh = LANES >> 5
-            for kvb in range(2):
-                kv = np.minimum(TK * j + 32 * kvb + krow, sh.nkv - 1)
-                for ks in range(KS):
-                    a = kb + kv * sh.k_nb1 + hh * 16 + ks * 32
-                    rs = kb + kv * sh.k_nb1
-                    _check((kv >= 0) & (kv < sh.nkv) & (a >= rs) & (a + 16 <= rs + ROW) & (a + 16 <= sh.kv_bytes()),
-                           "K load outside its row")
+    if sh.mode == "tensor":
+        ent = lambda row, pos: sh.mask[bb % sh.bm, h % sh.hm, row, pos]
+        for (T, j) in computed:
+            if cls[(1 if T == tB else 0, j)] == 3:
+                words = mask_words_kernel(sh, buf, plane_off, T, j, plant)
+                _check(words == mask_words_expected(sh, ent, T, j),
+                       f"mask words of block ({T}, {j}) differ from the entries")
     want = {(tB, j) for j in liveB} | {(tA, j) for j in liveA}
     _check(set(computed) == want and all(v == 1 for v in computed.values()),
            f"blocks computed {sorted(computed.items())} != live {sorted(want)}")
 
-    # V copies: every used tile, wavefront w issues parts w and w + 8
+    # K, then V copies: every used tile, wavefront w issues parts w and w + 8
+    # into the same LDS area; then the operand reads of each computed block
+    # (K: 16-byte A-operand reads, V^T: transposed 8-byte reads) must find the
+    # global chunk they need
     used = sorted(set(liveA) | set(liveB))
-    written = np.zeros(MAXK * VT, dtype=np.int32)
-    vsrc = np.full(MAXK * VT // 16, -1, dtype=np.int64)   # global chunk address landing in each LDS chunk
     rl = LANES >> 4
-    col = ((LANES & 15) ^ swz_v(rl)) * 16
-    for j in used:
-        kv0 = TK * j
-        for w in range(NW):
-            for gg in range(2):
-                g = w + NW * gg
-                r = 4 * g + rl
-                dst = j * VT + 4 * g * ROW
-                if kv0 + TK <= sh.nkv and plant != "v_clamp_always_full":
-                    ga = kb + kv0 * sh.k_nb1 + r * sh.k_nb1 + col
-                    kv = kv0 + r
-                else:
-                    kv = np.minimum(kv0 + r, sh.nkv - 1) if plant != "v_no_row_clamp" else kv0 + r
-                    ga = kb + kv * sh.k_nb1 + col
-                _check(kv < sh.nkv, f"V copy reads row {kv.max()} >= n_kv {sh.nkv}")
-                rs = kb + kv * sh.k_nb1
-                _check((ga >= rs) & (ga + 16 <= rs + ROW) & (ga + 16 <= sh.kv_bytes()), "V copy outside its row")
-                l = dst + 16 * LANES
-                _check((l >= 0) & (l + 16 <= MAXK * VT), "V copy lands outside the V area")
-                for x in range(16):
-                    np.add.at(written, l + x, 1)
-                vsrc[l // 16] = ga
-    for j in used:
-        _check(written[j * VT:(j + 1) * VT] == 1, f"V tile {j}: bytes written {written[j * VT:(j + 1) * VT].min()}.."
-               f"{written[j * VT:(j + 1) * VT].max()} times")
-    # V^T reads of each computed block: 8 bytes per lane, inside its tile, and
-    # the LDS chunk read holds the global chunk of row (kv) the operand needs
+    am, ahb, ab = (LANES & 31) >> 3, ((LANES & 31) >> 2) & 1, LANES & 3
+    krow = np.where(ahb != 0, 16 + ((am + 2) & 3) * 4 + ab, 4 * am + ab)
+    hh = LANES >> 5
     vq = (LANES & 15) >> 2
     clo = 2 * ((LANES & 31) >> 4) + ((LANES & 3) >> 1)
-    hh = LANES >> 5
-    for (T, j) in computed:
-        for pc in range(4):
-            kvb, cc = pc >> 1, pc & 1
-            for db in range(DB):
-                for hi in range(2):
-                    row_in_tile = np.where(hh != 0, 24 - 8 * cc, 8 * cc) + vq + 32 * kvb + 4 * hi
-                    vaddr = j * VT + row_in_tile * ROW + ((4 * db + clo) ^ swz_v(vq)) * 16 + (LANES & 1) * 8
-                    _check((vaddr >= j * VT) & (vaddr + 8 <= (j + 1) * VT), "V^T read outside its tile")
-                    _check(written[vaddr] == 1, "V^T read of an unwritten byte")
-                    # the chunk holds dims 8 c .. 8 c + 7 of the row, c = (4 db + clo)
-                    kvr = np.minimum(TK * j + row_in_tile, sh.nkv - 1)
-                    want = kb + kvr * sh.k_nb1 + (4 * db + clo) * 16
-                    _check(vsrc[vaddr // 16] == want, "V^T read finds another row or chunk than it needs")
+    for role in ("k", "v"):
+        swz = swz_k if role == "k" else swz_v
+        written = np.zeros(MAXK * VT, dtype=np.int32)
+        src = np.full(MAXK * VT // 16, -1, dtype=np.int64)   # global chunk address landing in each LDS chunk
+        for j in used:
+            kv0 = TK * j
+            for w in range(NW):
+                for gg in range(2):
+                    g = w + NW * gg
+                    r = 4 * g + rl
+                    col = ((LANES & 15) ^ swz(r)) * 16
+                    dst = j * VT + 4 * g * ROW
+                    if kv0 + TK <= sh.nkv and plant != "v_clamp_always_full":
+                        kv = kv0 + r
+                        ga = kb + kv0 * sh.k_nb1 + r * sh.k_nb1 + col
+                    else:
+                        kv = np.minimum(kv0 + r, sh.nkv - 1) if plant != "v_no_row_clamp" else kv0 + r
+                        ga = kb + kv * sh.k_nb1 + col
+                    _check(kv < sh.nkv, f"{role} copy reads row {kv.max()} >= n_kv {sh.nkv}")
+                    rs = kb + kv * sh.k_nb1
+                    _check((ga >= rs) & (ga + 16 <= rs + ROW) & (ga + 16 <= sh.kv_bytes()), f"{role} copy outside its row")
+                    l = dst + 16 * LANES
+                    _check((l >= 0) & (l + 16 <= MAXK * VT), f"{role} copy lands outside the LDS area")
+                    for x in range(16):
+                        np.add.at(written, l + x, 1)
+                    src[l // 16] = ga
+        for j in used:
+            seg = written[j * VT:(j + 1) * VT]
+            _check(seg == 1, f"{role} tile {j}: bytes written {seg.min()}..{seg.max()} times")
+        for (T, j) in computed:
+            if role == "k":
+                kx = hh ^ swz_k(krow)
+                for ks in range(KS):
+                    for kvb in range(2):
+                        addr = j * VT + krow * ROW + ((2 * ks) ^ kx) * 16 + 32 * kvb * ROW
+                        _check((addr >= j * VT) & (addr + 16 <= (j + 1) * VT), "K read outside its tile")
+                        kvr = np.minimum(TK * j + 32 * kvb + krow, sh.nkv - 1)
+                        want = kb + kvr * sh.k_nb1 + (2 * ks + hh) * 16
+                        _check(src[addr // 16] == want, "K operand read finds another row or chunk than it needs")
+            else:
+                for pc in range(4):
+                    kvb, cc = pc >> 1, pc & 1
+                    for db in range(DB):
+                        for hi in range(2):
+                            row_in_tile = np.where(hh != 0, 24 - 8 * cc, 8 * cc) + vq + 32 * kvb + 4 * hi
+                            vaddr = j * VT + row_in_tile * ROW + ((4 * db + clo) ^ swz_v(vq)) * 16 + (LANES & 1) * 8
+                            _check((vaddr >= j * VT) & (vaddr + 8 <= (j + 1) * VT), "V^T read outside its tile")
+                            _check(written[vaddr] == 1, "V^T read of an unwritten byte")
+                            kvr = np.minimum(TK * j + row_in_tile, sh.nkv - 1)
+                            want = kb + kvr * sh.k_nb1 + (4 * db + clo) * 16
+                            _check(src[vaddr // 16] == want, "V^T read finds another row or chunk than it needs")
 
-    # merge and store: tile T's wavefronts each take groups iT, iT + wT, ...
+    # merge and store: a wavefront of a tile with others publishes its 16
+    # groups (16-byte chunk (w, q, lane) at byte 16 (1024 w + 64 q + lane) of
+    # the V area); tile T's wavefronts each take groups iT, iT + wT, ... and
+    # read group q of every wavefront of the tile; a lone wavefront stores its
+    # own 16 groups
+    published = set()
+    for w in range(NW):
+        onB = w < wB
+        wT = wB if onB else NW - wB
+        if wT > 1:
+            for q in range(16):
+                off = 16 * (1024 * w + 64 * q + LANES)
+                _check((off >= 0) & (off + 16 <= MAXK * VT), "published chunk outside the V area")
+                published.add((w, q))
     for w in range(NW):
         onB = w < wB
         if not onB and not hasA:
@@ -381,7 +450,12 @@ def _emulate_wg(sh, p, h, bb, hk, bkv, nt, nk, buf, stored, plant):
         wT = wB if onB else NW - wB
         iT = w if onB else NW - 1 - w
         T = tB if onB else tA
+        g0 = 0 if onB else wB
         for q in range(iT, 16, wT):
+            if wT > 1:
+                for gi in range(NW):
+                    g = g0 + min(gi, wT - 1)
+                    _check((g, q) in published and ((g < wB) == onB), "merge reads a group nobody of the tile published")
             dbq, a4 = q >> 2, q & 3
             for lane in range(64):
                 row = 32 * T + (lane & 31)

@@ -62,6 +62,15 @@ def test_causal_439_one_block_per_wavefront():
         assert assignment(nA, nB, True) == nB
 
 
+def test_at_most_two_blocks_per_wavefront():
+    # up to 8 live KV tiles per query tile: no wavefront computes more than 2 blocks
+    from pair_emul import blocks_per_wave
+    for nA in range(9):
+        for nB in range(9):
+            assert blocks_per_wave(nA, nB, True) <= 2, (nA, nB)
+        assert blocks_per_wave(0, nA, False) <= 1
+
+
 @pytest.mark.parametrize("plant", ["no_chunk_clamp", "wb_off_by_one", "v_no_row_clamp"])
 def test_pair_emulation_catches_planted_mistakes(plant):
     with pytest.raises(Violation):

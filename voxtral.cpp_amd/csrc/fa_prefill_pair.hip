@@ -21,18 +21,22 @@
 //   Block classes: dead (skipped), all-zero mask (computed without the mask)
 //   or mixed (mask values added). With an implicit mask they follow from the
 //   formula; with a mask tensor each wavefront first reads the mask of two
-//   candidate blocks, (B, w) and (A, 7 - w), and classifies them.
+//   candidate blocks, (B, w) and (A, 7 - w), as whole row segments, and
+//   classifies them.
 //   Assignment: B's live blocks go to wavefronts 0 .. wB - 1, A's to the rest
 //   in reverse order (wB in proportion to the live counts), so under a causal
-//   mask each wavefront computes the block it classified, whose mask values
-//   are already in its registers. A wavefront with several blocks walks them
-//   with the online softmax.
+//   mask each wavefront computes the block it classified. With at most 8 live KV tiles per query tile
+//   no wavefront gets more than two blocks (checked for every pair of live
+//   counts on the CPU); it takes one max over both, so O needs no rescale.
 //   Merge: every wavefront publishes (O, m, l) to LDS; the wavefronts of a
 //   tile then each merge and store a quarter (or so) of its elements.
-// Memory: every live V tile of the pair goes to LDS once (direct
-//   global-to-LDS copies, 16 KiB per tile, at most 8), shared by both tiles'
-//   wavefronts; K rows go straight from global memory into the MFMA operand
-//   registers of the wavefront that uses them; Q of both tiles is rotated
+// Memory, in three phases through one 128 KiB LDS area: every live K tile of
+//   the pair is copied in once (direct global-to-LDS copies of whole rows,
+//   16 KiB per tile, at most 8) and the wavefronts compute S from it; after a
+//   barrier the V tiles are copied over them while the softmax runs; then
+//   O^T = V^T P^T. Both tiles' wavefronts share every tile. (K read straight
+//   into the operand registers measured slower: each load instruction touches
+//   32 B of each of 32 rows.) Q of both tiles is rotated
 //   (vxfa_flash_attn_ext_rope: ggml's rope mode 0 at each row's position),
 //   rounded to f16 (ggml's Q conversion) and staged in LDS.
 // MFMA layouts, the row-to-KV permutation within a 32-position block, the V
@@ -213,28 +217,57 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     // candidates of this wavefront (mask tensor): (B, wave) and (A, 7 - wave)
     const int jB = wave, jA = MAXK - 1 - wave;
     const bool candB = jB < nk, candA = hasA && jA < nk;
-    uint32_t mwB[2][8], mwA[2][8];
     uint32_t liveA = 0, liveB = 0, mixA = 0, mixB = 0;
     if constexpr (MM == 1) {
-        u32x4 chB[2][3], chA[2][3];
-        // (a candidate that does not exist reads tile B's or A's first block)
-        mw_issue(tB, candB ? jB : 0, chB);
-        mw_issue(tA, candA ? jA : 0, chA);
-        issue_q();   // after the mask loads: their wait does not include Q's
-        mw_finish(tB, candB ? jB : 0, chB, mwB);
-        mw_finish(tA, candA ? jA : 0, chA, mwA);
-        auto classify = [&](const uint32_t (&mw)[2][8]) -> int {
+        // A candidate's 32 rows are read as the 16-byte-aligned chunks that
+        // cover each row's 128-byte segment: nine lanes per row (lane 63
+        // idle), seven rows per load, five loads. A chunk past the row's last
+        // data granule is replaced by that granule; entries outside the
+        // segment, past n_kv or of rows past n_q are dropped in registers.
+        const int lr = lane / 9, lc = lane - 9 * (lane / 9);
+        auto cls_issue = [&](int T, int j, u32x4 (&cw)[5]) {
+#pragma unroll
+            for (int u = 0; u < 5; ++u) {
+                const int row = 32 * T + 7 * u + lr;
+                const bool ok = lr < 7 && 7 * u + lr < 32 && row < a.nq;
+                const char* rowp = mplane + (int64_t)(ok ? row : 0) * a.m_nb1;
+                const uintptr_t last = (reinterpret_cast<uintptr_t>(rowp) + 2 * (uintptr_t)a.nkv - 1) & ~(uintptr_t)15;
+                const char* seg = rowp + 2 * TK * j;
+                const char* pa = seg - (int)(reinterpret_cast<uintptr_t>(seg) & 15);
+                const int lim = (int)((intptr_t)last - (intptr_t)reinterpret_cast<uintptr_t>(pa));
+                cw[u] = *(const u32x4*)(pa + min(16 * lc, lim));
+            }
+        };
+        auto cls_eval = [&](int T, int j, const u32x4 (&cw)[5]) -> int {
             bool live = false, nonzero = false;
 #pragma unroll
-            for (int kvb = 0; kvb < 2; ++kvb)
+            for (int u = 0; u < 5; ++u) {
+                const int row = 32 * T + 7 * u + lr;
+                const bool ok = lr < 7 && 7 * u + lr < 32 && row < a.nq;
+                const char* rowp = mplane + (int64_t)(ok ? row : 0) * a.m_nb1;
+                const char* seg = rowp + 2 * TK * j;
+                const int e0 = (int)((seg - (int)(reinterpret_cast<uintptr_t>(seg) & 15) + 16 * lc) - rowp) / 2;
+                // entries k of the chunk inside [64 j, min(64 j + 64, n_kv))
+                const int lo = max(TK * j - e0, 0), hi = min(min(TK * j + TK, a.nkv) - e0, 8);
+                const uint32_t m8 = (ok && hi > lo) ? (((1u << hi) - 1u) & ~((1u << lo) - 1u)) : 0u;
 #pragma unroll
-                for (int w = 0; w < 8; ++w) {
-                    live |= mw[kvb][w] != 0xFC00FC00u;
-                    nonzero |= (mw[kvb][w] & 0x7FFF7FFFu) != 0u;
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t wm = (((m8 >> (2 * w)) & 1u) ? 0x0000FFFFu : 0u) |
+                                        (((m8 >> (2 * w + 1)) & 1u) ? 0xFFFF0000u : 0u);
+                    live |= ((cw[u][w] ^ 0xFC00FC00u) & wm) != 0u;
+                    nonzero |= (cw[u][w] & 0x7FFF7FFFu & wm) != 0u;
                 }
-            return !__any(live) ? 0 : __any(nonzero) ? 3 : 1;
+            }
+            const bool any_live = __any(live);
+            // a KV tile running past n_kv is mixed (its positions there are -inf)
+            return !any_live ? 0 : (__any(nonzero) || TK * j + TK > a.nkv) ? 3 : 1;
         };
-        const int cB = classify(mwB), cA = classify(mwA);
+        u32x4 cwB[5], cwA[5];
+        // (a candidate that does not exist reads tile B's or A's first block)
+        cls_issue(tB, candB ? jB : 0, cwB);
+        cls_issue(tA, candA ? jA : 0, cwA);
+        issue_q();   // after the mask loads: their wait does not include Q's
+        const int cB = cls_eval(tB, candB ? jB : 0, cwB), cA = cls_eval(tA, candA ? jA : 0, cwA);
         if (lane == 0) {
             if (candB) s_cls[MAXK + jB] = (uint8_t)cB;
             if (candA) s_cls[jA] = (uint8_t)cA;
@@ -294,86 +327,60 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
         return 0;
     };
 
-    // ---- K of the first block: A-operand rows straight from global memory ----
-    // (row nl of 32-block kvb is K row krow of it; chunk 2 ks + hh)
-    const int krow = [&] {
-        const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
-        return ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
-    }();
-    half8 kr[2][KS];
-    auto issue_k = [&](int j) {
-#pragma unroll
-        for (int kvb = 0; kvb < 2; ++kvb) {
-            const int kv = min(TK * j + 32 * kvb + krow, a.nkv - 1);
-            const char* kp = kb + (int64_t)kv * a.k_nb1 + hh * 16;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[kvb][ks] = *(const half8*)(kp + ks * 32);
-        }
-    };
-    // mask words of the first block: the classification's when it is one of
-    // this wavefront's candidates, else read again (finished after the wait
-    // below, so the V copies are not held back by them)
-    uint32_t mw[2][8];
-    u32x4 chr[2][3];
-    bool reload = false;
-    int j0 = 0;
-    if (nblk > 0) {
-        j0 = block_tile(0);
-        issue_k(j0);
-        if ((mix >> j0) & 1u) {
-            if constexpr (MM == 1) {
-                if (onB && j0 == jB) {
-#pragma unroll
-                    for (int kvb = 0; kvb < 2; ++kvb)
-#pragma unroll
-                        for (int w = 0; w < 8; ++w) mw[kvb][w] = mwB[kvb][w];
-                } else if (!onB && j0 == jA) {
-#pragma unroll
-                    for (int kvb = 0; kvb < 2; ++kvb)
-#pragma unroll
-                        for (int w = 0; w < 8; ++w) mw[kvb][w] = mwA[kvb][w];
-                } else {
-                    mw_issue(T, j0, chr);
-                    reload = true;
-                }
-            } else {
-                mw_formula(T, j0, mw);
-            }
-        }
+    // ---- the wavefront's blocks (at most two) and their mask words ----------
+    // (mask tensor: the words of a mixed block in the accumulator layout are
+    // read here and finished after the wait below; implicit: the formula)
+    const int j0 = nblk > 0 ? block_tile(0) : 0;
+    const int j1 = nblk > 1 ? block_tile(1) : 0;
+    const bool mix0 = nblk > 0 && ((mix >> j0) & 1u);
+    const bool mix1 = nblk > 1 && ((mix >> j1) & 1u);
+    uint32_t mw0[2][8], mw1[2][8];
+    u32x4 chr0[2][3], chr1[2][3];
+    if (mix0) {
+        if constexpr (MM == 1) mw_issue(T, j0, chr0);
+        else mw_formula(T, j0, mw0);
+    }
+    if (mix1) {
+        if constexpr (MM == 1) mw_issue(T, j1, chr1);
+        else mw_formula(T, j1, mw1);
     }
 
-    // ---- V: every live KV tile of the pair into LDS, once ---------------------
+    // ---- K, then V: every live KV tile of the pair through one LDS area -----
     // Tile j's rows 4 g .. 4 g + 3 (g = 0..15) are one copy instruction;
     // wavefront w issues g = w and w + 8 of every tile. Lane l writes LDS
     // chunk l % 16 of row 4 g + l / 16, which holds the row's chunk
-    // (l % 16) ^ swizzle(row). Rows past n_kv repeat row n_kv - 1.
+    // (l % 16) ^ swizzle(row) (the K or the V swizzle). Rows past n_kv repeat
+    // row n_kv - 1.
     const uint32_t used = liveA | liveB;
-    {
-        const uint32_t lds_v = lds_offset(sV);
-        const int rl = lane >> 4;
-        const int col = ((lane & 15) ^ swz_v<D>(rl)) * 16;   // swizzle depends on row % 4 = rl
-        for (int j = 0; j < nk; ++j) {
-            if (!((used >> j) & 1u)) continue;
-            const int kv0 = TK * j;
+    const uint32_t lds_kv = lds_offset(sV);
+    const int rl = lane >> 4;
+    auto issue_tiles = [&](const char* base, int64_t nb1, auto is_k) {
+        for (int jt = 0; jt < nk; ++jt) {
+            if (!((used >> jt) & 1u)) continue;
+            const int kv0 = TK * jt;
 #pragma unroll
             for (int gg = 0; gg < 2; ++gg) {
                 const int g = wave + NW * gg;
                 const int r = 4 * g + rl;
-                const uint32_t dst = lds_v + j * VT + 4 * g * ROW;
+                const int col = ((lane & 15) ^ (decltype(is_k)::value ? swz_k<D>(r) : swz_v<D>(r))) * 16;
+                const uint32_t dst = lds_kv + jt * VT + 4 * g * ROW;
                 if (kv0 + TK <= a.nkv) {
-                    dma16(vb + (int64_t)kv0 * a.v_nb1, (uint32_t)r * (uint32_t)a.v_nb1 + col, dst);
+                    dma16(base + (int64_t)kv0 * nb1, (uint32_t)r * (uint32_t)nb1 + col, dst);
                 } else {
                     const int kv = min(kv0 + r, a.nkv - 1);
-                    dma16_addr(vb + (int64_t)kv * a.v_nb1 + col, dst);
+                    dma16_addr(base + (int64_t)kv * nb1 + col, dst);
                 }
             }
         }
-    }
+    };
+    issue_tiles(kb, a.k_nb1, std::true_type{});
 
     // ---- Q: wait for every load, round to f16, stage -------------------------
     wait_all_mem();
-    if constexpr (MM == 1)
-        if (reload) mw_finish(T, j0, chr, mw);
+    if constexpr (MM == 1) {
+        if (mix0) mw_finish(T, j0, chr0, mw0);
+        if (mix1) mw_finish(T, j1, chr1, mw1);
+    }
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         const int i = tid + NT * u;
@@ -394,11 +401,87 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
             *(half4*)(qrow + (((cch >> 1) ^ (r & 15)) * 16) + (cch & 1) * 8) = v;
         }
     }
-    __syncthreads();   // Q staged, V tiles visible
+    __syncthreads();   // Q staged, K tiles visible
 
-    // ---- blocks ----------------------------------------------------------------
+    // ---- S^T = K Q^T of the wavefront's blocks, K operands from LDS ----------
+    // (A-operand row nl of 32-block kvb is K row krow of it, chunk 2 ks + hh)
+    int kaddr[KS];
+    {
+        const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
+        const int krow = ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
+        const int kx = hh ^ swz_k<D>(krow);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kaddr[ks] = krow * ROW + ((2 * ks) ^ kx) * 16;
+    }
+    const char* qs = sQ + (onB ? QT : 0) + nl * ROW;
+    floatx16 S0[2], S1[2];
+    auto s_block = [&](int jt, floatx16 (&S)[2]) {
+        const char* kt = sV + jt * VT;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 qk = *(const half8*)(qs + (((2 * ks + hh) ^ (nl & 15)) * 16));
+#pragma unroll
+            for (int kvb = 0; kvb < 2; ++kvb) {
+                const half8 kk = *(const half8*)(kt + kaddr[ks] + 32 * kvb * ROW);
+                S[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kk, qk, ks == 0 ? floatx16{} : S[kvb], 0, 0, 0);
+            }
+        }
+    };
+    if (nblk > 0) s_block(j0, S0);
+    if (nblk > 1) s_block(j1, S1);
+    __syncthreads();   // every K read done: the area takes the V tiles
+    issue_tiles(vb, a.v_nb1, std::false_type{});
+
+    // ---- softmax over the wavefront's blocks (while V lands) ------------------
+    // scores in log2 units with the mask added (-inf stays -inf); one max over
+    // both blocks, so O needs no rescale
+    auto scores = [&](floatx16 (&S)[2], bool mixed, const uint32_t (&mwx)[2][8]) -> float {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) {
+                float x = S[kvb][jj] * c;
+                if (mixed) {
+                    const half2 m2 = __builtin_bit_cast(half2, mwx[kvb][jj >> 1]);
+                    x = fmaf((float)m2[jj & 1], kLog2e, x);
+                }
+                S[kvb][jj] = x;
+                mx = fmaxf(mx, x);
+            }
+        return mx;
+    };
+    float mx = -INFINITY;
+    if (nblk > 0) mx = scores(S0, mix0, mw0);
+    if (nblk > 1) mx = fmaxf(mx, scores(S1, mix1, mw1));
+    const float m_run = pair32_max(mx);
+    const float ms = (m_run == -INFINITY) ? 0.f : m_run;
+    const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    half8 P0[4], P1[4];
+    float ls[2] = {0.f, 0.f};
+    auto probs = [&](const floatx16 (&S)[2], half8 (&P)[4]) {
+#pragma unroll
+        for (int pc = 0; pc < 4; ++pc) {
+            const int kvb = pc >> 1, cc = pc & 1;
+#pragma unroll
+            for (int i2 = 0; i2 < 8; ++i2) P[pc][i2] = (_Float16)exp2_fast(S[kvb][8 * cc + i2] - ms);
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const half2 p2 = {P[pc][2 * i2], P[pc][2 * i2 + 1]};
+                ls[i2 & 1] = __builtin_amdgcn_fdot2(p2, ones, ls[i2 & 1], false);
+            }
+        }
+    };
+    if (nblk > 0) probs(S0, P0);
+    if (nblk > 1) probs(S1, P1);
+    const float l_run = ls[0] + ls[1];
+    wait_all_mem();
+    __syncthreads();   // V tiles visible
+
+    // ---- O^T = V^T P^T -------------------------------------------------------
     floatx16 o[DB];
-    float m_run = -INFINITY, l_run = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = floatx16{};
     const int vq = (lane & 15) >> 2;
     const int clo = 2 * ((lane & 31) >> 4) + ((lane & 3) >> 1);
     int vaddr[2][DB];
@@ -408,130 +491,94 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
         for (int db = 0; db < DB; ++db)
             vaddr[cc][db] = ((hh ? 24 - 8 * cc : 8 * cc) + vq) * ROW + ((4 * db + clo) ^ swz_v<D>(vq)) * 16 +
                             (lane & 1) * 8;
-    const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-    const char* qs = sQ + (onB ? QT : 0) + nl * ROW;
-    // One block at KV tile j. FIRST: O starts at zero (the first PV MFMAs take
-    // a zero accumulator) and no rescale; O is not live before them. The Q
-    // operand of each k-step is read from LDS right before its two MFMAs.
-    auto run_block = [&](auto first_tag, int j, bool mixed) {
-        constexpr bool FIRST = decltype(first_tag)::value;
-        floatx16 S[2];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const half8 qk = *(const half8*)(qs + (((2 * ks + hh) ^ (nl & 15)) * 16));
-#pragma unroll
-            for (int kvb = 0; kvb < 2; ++kvb)
-                S[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[kvb][ks], qk, ks == 0 ? floatx16{} : S[kvb], 0, 0, 0);
-        }
-        // scores in log2 units, the mask added (-inf stays -inf)
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kvb = 0; kvb < 2; ++kvb)
-#pragma unroll
-            for (int jj = 0; jj < 16; ++jj) {
-                float x = S[kvb][jj] * c;
-                if (mixed) {
-                    const half2 m2 = __builtin_bit_cast(half2, mw[kvb][jj >> 1]);
-                    x = fmaf((float)m2[jj & 1], kLog2e, x);
-                }
-                S[kvb][jj] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = pair32_max(mx);
-        const float mnew = fmaxf(m_run, mx);
-        const float ms = (mnew == -INFINITY) ? 0.f : mnew;
-        if constexpr (!FIRST) {
-            const float alpha = exp2_fast(m_run - ms);
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int jj = 0; jj < 16; ++jj) o[db][jj] *= alpha;
-            l_run *= alpha;
-        }
-        m_run = mnew;
-        const char* vt = sV + j * VT;
-        float ls[2] = {0.f, 0.f};
+    auto pv_block = [&](int jt, const half8 (&P)[4]) {
+        const char* vt = sV + jt * VT;
 #pragma unroll
         for (int pc = 0; pc < 4; ++pc) {
             const int kvb = pc >> 1, cc = pc & 1;
-            half8 pb;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) pb[i] = (_Float16)exp2_fast(S[kvb][8 * cc + i] - ms);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const half2 p2 = {pb[2 * i], pb[2 * i + 1]};
-                ls[i & 1] = __builtin_amdgcn_fdot2(p2, ones, ls[i & 1], false);
-            }
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 const char* vp = vt + vaddr[cc][db] + 32 * kvb * ROW;
                 const half4 lo4 = lds_read_tr16(vp);
                 const half4 hi4 = lds_read_tr16(vp + 4 * ROW);
                 const half8 va = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, (FIRST && pc == 0) ? floatx16{} : o[db], 0,
-                                                               0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, P[pc], o[db], 0, 0, 0);
             }
         }
-        l_run += ls[0] + ls[1];
     };
-    if (nblk > 0) {
-        run_block(std::true_type{}, j0, ((mix >> j0) & 1u) != 0);
-        for (int k = 1; k < nblk; ++k) {
-            const int j = block_tile(k);
-            const bool mixed = ((mix >> j) & 1u) != 0;
-            issue_k(j);
-            if (mixed) {
-                if constexpr (MM == 1) {
-                    u32x4 ch[2][3];
-                    mw_issue(T, j, ch);
-                    mw_finish(T, j, ch, mw);
-                } else {
-                    mw_formula(T, j, mw);
-                }
-            }
-            run_block(std::false_type{}, j, mixed);
-        }
-    } else {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db] = floatx16{};
-    }
+    if (nblk > 0) pv_block(j0, P0);
+    if (nblk > 1) pv_block(j1, P1);
 
     // ---- merge each tile over its wavefronts, normalise, store ---------------
+    // Output group q = 4 db + a4 of a lane is accumulator quad a4 of O^T block
+    // db: dims 32 db + 8 a4 + 4 hh .. + 3 of row 32 T + nl. A wavefront whose
+    // tile has other wavefronts publishes its 16 groups as 16-byte chunks
+    // (group q of lane l at float 4 (64 q + l) of its 16 KiB) with its m and l;
+    // the tile's wavefronts then each merge groups iT, iT + wT, ... over all
+    // of them, in wavefront order. A tile with one wavefront stores its own.
+    const int row = 32 * T + nl;
+    float* out_row = a.dst + (((int64_t)b * a.nq + (row < a.nq ? row : 0)) * a.hq + h) * D + 4 * hh;
     __syncthreads();   // every V read done: the V area takes the published O
-    {
-        float* pub = (float*)sV + wave * (NE * 64);
+    if (wT > 1) {
+        floatx4* pub = (floatx4*)sV + wave * (16 * 64) + lane;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int jj = 0; jj < 16; ++jj) pub[(16 * db + jj) * 64 + lane] = o[db][jj];
+        for (int q = 0; q < 16; ++q) {
+            const int db = q >> 2, a4 = q & 3;
+            pub[q * 64] = floatx4{o[db][4 * a4], o[db][4 * a4 + 1], o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
+        }
         s_ml[wave * 64 + lane] = m_run;
         s_ml[NW * 64 + wave * 64 + lane] = l_run;
     }
     __syncthreads();
-    // the tile's wavefronts: B's are 0 .. wB - 1, A's wB .. NW - 1
-    const int g0 = onB ? 0 : wB;
-    float M = -INFINITY;
-    for (int g = g0; g < g0 + wT; ++g) M = fmaxf(M, s_ml[g * 64 + lane]);
-    const float Ms = (M == -INFINITY) ? 0.f : M;
-    float lsum = 0.f;
-    for (int g = g0; g < g0 + wT; ++g) lsum = fmaf(exp2_fast(s_ml[g * 64 + lane] - Ms), s_ml[NW * 64 + g * 64 + lane], lsum);
-    const float lt = pair32_sum(lsum);
-    const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
-    const int row = 32 * T + nl;
-    // 16 groups of 4 elements (O^T block db, accumulator quad a4: dims
-    // 32 db + 8 a4 + 4 hh .. + 3); this wavefront takes groups iT, iT + wT, ...
-    for (int q = iT; q < 16; q += wT) {
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int g = g0; g < g0 + wT; ++g) {
-            const float wg = exp2_fast(s_ml[g * 64 + lane] - Ms) * inv;
-            const float* src = (const float*)sV + g * (NE * 64) + (4 * q) * 64 + lane;
-#pragma unroll
-            for (int e2 = 0; e2 < 4; ++e2) acc[e2] = fmaf(wg, src[e2 * 64], acc[e2]);
-        }
+    if (wT == 1) {
+        const float lt = pair32_sum(l_run);
+        const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
         if (row < a.nq) {
-            const int db = q >> 2, a4 = q & 3;
-            float* out = a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 32 * db + 8 * a4 + 4 * hh;
-            *(floatx4*)out = acc;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int db = q >> 2, a4 = q & 3;
+                *(floatx4*)(out_row + 32 * db + 8 * a4) =
+                    floatx4{o[db][4 * a4] * inv, o[db][4 * a4 + 1] * inv, o[db][4 * a4 + 2] * inv,
+                            o[db][4 * a4 + 3] * inv};
+            }
+        }
+    } else {
+        // the tile's wavefronts: B's are 0 .. wB - 1, A's wB .. NW - 1; slots
+        // past wT repeat the last one with weight 0
+        const int g0 = onB ? 0 : wB;
+        float mg[NW], lg[NW];
+#pragma unroll
+        for (int gi = 0; gi < NW; ++gi) {
+            const int g = g0 + min(gi, wT - 1);
+            mg[gi] = s_ml[g * 64 + lane];
+            lg[gi] = s_ml[NW * 64 + g * 64 + lane];
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int gi = 0; gi < NW; ++gi) M = fmaxf(M, mg[gi]);
+        const float Ms = (M == -INFINITY) ? 0.f : M;
+        float wg[NW];
+        float lsum = 0.f;
+#pragma unroll
+        for (int gi = 0; gi < NW; ++gi) {
+            wg[gi] = gi < wT ? exp2_fast(mg[gi] - Ms) : 0.f;
+            lsum = fmaf(wg[gi], lg[gi], lsum);
+        }
+        const float lt = pair32_sum(lsum);
+        const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
+#pragma unroll
+        for (int gi = 0; gi < NW; ++gi) wg[gi] *= inv;
+        const floatx4* src = (const floatx4*)sV + lane;
+        for (int q = iT; q < 16; q += wT) {
+            floatx4 part[NW];
+#pragma unroll
+            for (int gi = 0; gi < NW; ++gi) part[gi] = src[(g0 + min(gi, wT - 1)) * (16 * 64) + q * 64];
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int gi = 0; gi < NW; ++gi)
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) acc[e2] = fmaf(wg[gi], part[gi][e2], acc[e2]);
+            if (row < a.nq) *(floatx4*)(out_row + 32 * (q >> 2) + 8 * (q & 3)) = acc;
         }
     }
 }
