@@ -88,6 +88,17 @@ struct FastDiv {
 // XCD's L2 for the head's K and V. All constants come from the host, so the
 // kernel's first global loads wait on one batch of argument loads and no
 // division.
+// n / d and n % d for 0 <= n < 2^31, d fixed per launch and set up on the host
+// (a division by a run-time value is a long scalar sequence on the GPU, run
+// by every wavefront before its first load)
+struct DivMod {
+    uint32_t d;
+    FastDiv f;
+    static DivMod make(uint32_t d) { return DivMod{d, FastDiv::make(d)}; }
+    __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const { return f.div(n); }
+    __host__ __device__ __forceinline__ uint32_t mod(uint32_t n) const { return n - d * f.div(n); }
+};
+
 struct GridMap {
     uint32_t q8, r8;          // nwg / 8, nwg % 8
     uint32_t nqt, hq;

@@ -127,8 +127,14 @@ __global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
     }
 }
 
+// the divisors of one decode launch: kv heads, splits, q batches per kv
+// batch, mask head planes, mask batches
+struct DecodeDivs {
+    DivMod hkv, split, bgrp, hm, bm;
+};
+
 template <int D, int G, bool QF16, bool MASK, bool KV32>
-__global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
+__global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs dv) {
     static_assert(D == 64 || D == 128, "head dim");
     static_assert(G == 1 || G == 2 || G == 4, "GQA group");
     constexpr int KS = D / 32;        // MFMA k-steps of 32 dims
@@ -150,10 +156,10 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int g = blockIdx.x % a.hkv;
-    const int split = blockIdx.x / a.hkv;
+    const int g = (int)dv.hkv.mod(blockIdx.x);
+    const int split = (int)dv.hkv.div(blockIdx.x);
     const int b = blockIdx.y;
-    const int bkv = b / (a.b / a.bk);
+    const int bkv = (int)dv.bgrp.div(b);
     constexpr bool masked = MASK;  // compile time, like QF16, so no load is conditional at run time
     // rotary position of the query token (also the appended row's: the host
     // requires one kv batch per q batch), requested before any other load. A
@@ -176,8 +182,8 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     // batch b % bm. One scan when they are one plane or consecutive planes.
     int lo = a.kv_lo, hi = a.kv_hi;   // without a mask tensor the host gives the live range
     if constexpr (masked) {
-        const char* mb = (const char*)a.mask + (int64_t)(b % a.bm) * a.m_nb3;
-        const int p0 = (g * G) % a.hm;
+        const char* mb = (const char*)a.mask + (int64_t)dv.bm.mod(b) * a.m_nb3;
+        const int p0 = (int)dv.hm.mod(g * G);
         const int np = a.hm == 1 ? 1 : (p0 + G <= a.hm ? G : 0);
         if (np > 0) {
             mask_live_range<DEC_THREADS>((const uint16_t*)(mb + (int64_t)p0 * a.m_nb2), a.m_nb2, np, a.nkv, lds_red,
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
             hi = 0;
             for (int j = 0; j < G; ++j) {
                 int l1, h1;
-                mask_live_range<DEC_THREADS>((const uint16_t*)(mb + (int64_t)((g * G + j) % a.hm) * a.m_nb2), 0, 1,
+                mask_live_range<DEC_THREADS>((const uint16_t*)(mb + (int64_t)dv.hm.mod(g * G + j) * a.m_nb2), 0, 1,
                                              a.nkv, lds_red, l1, h1);
                 if (h1 > l1) { lo = min(lo, l1); hi = max(hi, h1); }
             }
@@ -202,8 +208,15 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
     const int hi_main = a.append ? min(hi, a.nkv - 1) : hi;
     const int span = max(hi_main - lo, 0);
     const int ntiles = (span + TP - 1) / TP;
-    const int t_begin = (int)(((int64_t)ntiles * split) / a.n_split);
-    const int t_end = (int)(((int64_t)ntiles * (split + 1)) / a.n_split);
+    // (ntiles * n_split < 2^31 but for caches of more than 2^30 positions)
+    int t_begin, t_end;
+    if (ntiles < (1 << 25)) {
+        t_begin = (int)dv.split.div((uint32_t)(ntiles * split));
+        t_end = (int)dv.split.div((uint32_t)(ntiles * (split + 1)));
+    } else {
+        t_begin = (int)(((int64_t)ntiles * split) / a.n_split);
+        t_end = (int)(((int64_t)ntiles * (split + 1)) / a.n_split);
+    }
 
     const char* kb = (const char*)a.k + (int64_t)g * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)g * a.v_nb2 + (int64_t)bkv * a.v_nb3;
@@ -212,8 +225,8 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hq = g * G + (i % G);
-            mplane[i] = (const uint16_t*)((const char*)a.mask + (int64_t)(hq % a.hm) * a.m_nb2 +
-                                          (int64_t)(b % a.bm) * a.m_nb3);
+            mplane[i] = (const uint16_t*)((const char*)a.mask + (int64_t)dv.hm.mod(hq) * a.m_nb2 +
+                                          (int64_t)dv.bm.mod(b) * a.m_nb3);
         }
     }
 
@@ -548,12 +561,14 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a) {
 template <int D, int G, bool KV32>
 static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
     const dim3 grid(a.n_split * a.hkv, a.b), block(DEC_THREADS);
+    const DecodeDivs dv = {DivMod::make(a.hkv), DivMod::make(a.n_split), DivMod::make(a.b / a.bk),
+                           DivMod::make(a.hm > 0 ? a.hm : 1), DivMod::make(a.bm > 0 ? a.bm : 1)};
     if (a.mask) {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32>), grid, block, 0, st, a);
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32>), grid, block, 0, st, a, dv);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32>), grid, block, 0, st, a, dv);
     } else {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32>), grid, block, 0, st, a);
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32>), grid, block, 0, st, a, dv);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32>), grid, block, 0, st, a, dv);
     }
     if (a.n_split > 1)
         hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G * (D / 32), a.b), dim3(64), 0, st, a);
