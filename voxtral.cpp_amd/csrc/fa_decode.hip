@@ -273,6 +273,10 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
         const int r = pos + a.ring_start;
         return r >= a.ring_cap ? r - a.ring_cap : r;
     };
+    // f16 K/V tiles are read once per step: nontemporal loads without a mask
+    // tensor (measured 12.65 -> 12.37 us per layer at n_kv 8192 on one box,
+    // 12.66 -> 12.60 on another); with one (the ragged batch) and for the F32
+    // cache they measured ~1 % slower, so those keep ordinary loads
     auto load_tile = [&](Tile& T, int t) {
         const int p0 = lo + t * TP;
         const int pend = min(p0 + TP, hi_main);
@@ -285,8 +289,10 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
                 if constexpr (KV32) {
                     T.k[grp][ks][0] = *(const floatx4*)(kp + 128 * ks);
                     T.k[grp][ks][1] = *(const floatx4*)(kp + 128 * ks + 16);
-                } else {
+                } else if constexpr (masked) {
                     T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
+                } else {
+                    T.k[grp][ks] = __builtin_nontemporal_load((const half8*)(kp + 64 * ks));
                 }
             }
             if constexpr (masked) {
@@ -301,8 +307,10 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
             if constexpr (KV32) {
                 T.v[i][0] = *(const floatx4*)(vp);
                 T.v[i][1] = *(const floatx4*)(vp + 16);
-            } else {
+            } else if constexpr (masked) {
                 T.v[i] = *(const half8*)(vp);
+            } else {
+                T.v[i] = __builtin_nontemporal_load((const half8*)(vp));
             }
         }
     };

@@ -166,6 +166,8 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     // Staged in LDS as f16 rows of 128 bytes, 16-byte chunk j of row r at
     // position j ^ (r & 7). F32 Q: thread i takes 16-byte chunks i + NT u of
     // the BM x 16 chunks; F16 Q: of the BM x 8 chunks.
+    // Q is read once and O written once (whole 256-byte rows): nontemporal
+    // loads and stores (21.7 -> 20.3 us per layer measured on one box).
     constexpr int QCH = QF16 ? 8 : 16;         // 16-byte global chunks per row
     constexpr int QPT = BM * QCH / NT;         // per thread
     floatx4 qraw[QPT];
@@ -176,8 +178,8 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         const int row = qw0 + r;
         qraw[u] = floatx4{0.f, 0.f, 0.f, 0.f};
         if (row < a.nq)
-            qraw[u] = *(const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 + (int64_t)h * a.q_nb2 +
-                                        (int64_t)b * a.q_nb3 + cch * 16);
+            qraw[u] = __builtin_nontemporal_load((const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 +
+                                                                  (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3 + cch * 16));
     }
 
     // ---- block loads: global -> LDS ring -------------------------------------
@@ -581,7 +583,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         const int row = qw0 + r;
         if (row < a.nq) {
             const floatx4 v = *(const floatx4*)(ost + r * 256 + ((ch ^ (r & 15)) * 16));
-            *(floatx4*)(a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 4 * ch) = v;
+            __builtin_nontemporal_store(v, (floatx4*)(a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 4 * ch));
         }
     }
 }
