@@ -209,7 +209,8 @@ typedef struct vxfa_ring {
  * and written to its ring row in the same launch (as
  * vxfa_flash_attn_ext_append). The result equals vxfa_flash_attn_ext on a
  * linear cache holding the same rows in logical order. Single-token decode
- * with GQA group 1, 2 or 4 only (else VXFA_UNSUPPORTED). No counterpart in
+ * with GQA group 1, 2 or 4 only, capacity below 2^24 rows and capacity *
+ * row stride below 2 GiB (else VXFA_UNSUPPORTED). No counterpart in
  * ggml's op: it replaces the host-side shift plus the attention node. */
 int vxfa_flash_attn_ext_ring(vxfa_ctx* ctx, const vxfa_tensor* q,
                              vxfa_tensor* k, vxfa_tensor* v,

@@ -155,7 +155,9 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform (a scalar register): tile indices, row bases and loop
+    // bounds derived from it stay on the scalar unit
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = (int)dv.hkv.mod(blockIdx.x);
     const int split = (int)dv.hkv.div(blockIdx.x);
     const int b = blockIdx.y;
@@ -277,13 +279,40 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     // tensor (measured 12.65 -> 12.37 us per layer at n_kv 8192 on one box,
     // 12.66 -> 12.60 on another); with one (the ragged batch) and for the F32
     // cache they measured ~1 % slower, so those keep ordinary loads
+    // Addresses: a wave-uniform 64-bit row base (scalar registers) plus a
+    // 32-bit lane offset, row * stride + column bytes by one 24-bit
+    // multiply-add (the host keeps strides and ring sizes below 2^24 and a
+    // ring's span below 2^31 bytes). Positions p0 + x of a tile clamp to its
+    // last live position q; the tile's base row is that of position bp and
+    // lane x reads row bp + min(x, lim). A whole tile (lim = TP - 1, no ring
+    // wrap inside) reads rows bp + x: the lane offsets are the loop-invariant
+    // ones below and every per-row step goes into the scalar base. A tile
+    // that wraps round the ring takes the cache start as its base and
+    // absolute rows as offsets.
+    const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
+    const uint32_t koff0 = __umul24((uint32_t)(lane & 15), knb) + kcol * ESZ;
+    const uint32_t voff0 = __umul24((uint32_t)vrow, vnb) + vcol * ESZ;
     auto load_tile = [&](Tile& T, int t) {
         const int p0 = lo + t * TP;
-        const int pend = min(p0 + TP, hi_main);
+        const int q = min(p0 + TP, hi_main) - 1;
+        const int bp = q >= p0 ? p0 : max(q, 0);
+        const int lim = q >= p0 ? q - p0 : 0;
+        const int rb = row_of(bp);
+        const bool wrap = a.ring_cap > 0 && rb + lim >= a.ring_cap;
+        const bool whole = !wrap && lim == TP - 1;
+        auto row_off = [&](int x, uint32_t nb) {
+            const int rel = min(x, lim);
+            int r = rel;
+            if (wrap) r = rb + rel >= a.ring_cap ? rb + rel - a.ring_cap : rb + rel;
+            return __umul24((uint32_t)r, nb);
+        };
+        const char* kt = wrap ? kb : kb + (int64_t)rb * a.k_nb1;
+        const char* vt = wrap ? vb : vb + (int64_t)rb * a.v_nb1;
 #pragma unroll
         for (int grp = 0; grp < NG; ++grp) {
-            const int pos = max(min(p0 + 16 * grp + (lane & 15), pend - 1), 0);
-            const char* kp = kb + (int64_t)row_of(pos) * a.k_nb1 + kcol * ESZ;
+            const char* kbase = whole ? kt + (int64_t)(16 * grp) * a.k_nb1 : kt;
+            const uint32_t ko = whole ? koff0 : row_off(16 * grp + (lane & 15), knb) + kcol * ESZ;
+            const char* kp = kbase + ko;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if constexpr (KV32) {
@@ -296,14 +325,16 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
                 }
             }
             if constexpr (masked) {
+                const uint32_t pos = (uint32_t)(bp + min(16 * grp + (lane & 15), lim));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) T.m[grp][i] = mplane[i][pos];
             }
         }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int pos = max(min(p0 + vrow + i * RPI, pend - 1), 0);
-            const char* vp = vb + (int64_t)row_of(pos) * a.v_nb1 + vcol * ESZ;
+            const char* vbase = whole ? vt + (int64_t)(i * RPI) * a.v_nb1 : vt;
+            const uint32_t vo = whole ? voff0 : row_off(vrow + i * RPI, vnb) + vcol * ESZ;
+            const char* vp = vbase + vo;
             if constexpr (KV32) {
                 T.v[i][0] = *(const floatx4*)(vp);
                 T.v[i][1] = *(const floatx4*)(vp + 16);
@@ -517,24 +548,64 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     }
 
     // ---- merge lanes, then wavefronts ------------------------------------
+    // Each of the 8 G sums acc[h][j] (value v = 8 h + j) is reduced over the
+    // lanes sharing lane % CH. For CH = 16 by two cross-lane swap rounds on
+    // the VALU (no LDS round trips), four values per register at the end:
+    //   v_permlane32_swap(a, b) -> {[a_lo, b_lo], [a_hi, b_hi]} (32-lane
+    //   halves), summed: lanes 0-31 hold a partial of a, 32-63 one of b;
+    //   v_permlane16_swap(a, b) -> {[a0, b0, a2, b2], [a1, b1, a3, b3]}
+    //   (16-lane rows), summed: rows hold [a0+a1, b0+b1, a2+a3, b2+b3].
+    // Register j then holds value 4 j + perm(r) in row r, perm = (0, 2, 1, 3),
+    // and lane (r, c) stores it to slot 4 j + r, column c, of the wavefront's
+    // [8 G][16] LDS block (value v sits in slot (v & ~3) | perm(v & 3)).
+    float* const lds_sum = &lds_acc[0][0][0];
+    auto perm2 = [](int x) { return ((x & 1) << 1) | ((x >> 1) & 1); };
+    if constexpr (CH == 16) {
+        constexpr int NVAL = 8 * G;
+        float s1[NVAL / 2];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float s = acc[h][j];
-#pragma unroll
-            for (int m = CH; m < 64; m <<= 1) s += shfl_xor(s, m);
-            acc[h][j] = s;
+        for (int k = 0; k < NVAL / 2; ++k) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, acc[(2 * k) / 8][(2 * k) % 8]),
+                                                            __builtin_bit_cast(int, acc[(2 * k + 1) / 8][(2 * k + 1) % 8]),
+                                                            false, false);
+            s1[k] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
         }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) l_run[i] = row16_sum(l_run[i]);
-
-    if (lane < CH) {
+        for (int j = 0; j < NVAL / 4; ++j) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, s1[2 * j]),
+                                                            __builtin_bit_cast(int, s1[2 * j + 1]), false, false);
+            lds_sum[(wave * NVAL + 4 * j + (lane >> 4)) * 16 + (lane & 15)] =
+                __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+        }
+    } else {
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) lds_acc[wave][h][lane * 8 + j] = acc[h][j];
+            for (int j = 0; j < 8; ++j) {
+                float s = acc[h][j];
+#pragma unroll
+                for (int m = CH; m < 64; m <<= 1) s += shfl_xor(s, m);
+                acc[h][j] = s;
+            }
+        if (lane < CH) {
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) lds_acc[wave][h][lane * 8 + j] = acc[h][j];
+        }
     }
+    // wavefront w's sum for head h, dim d
+    auto acc_at = [&](int w, int h, int d) {
+        if constexpr (CH == 16) {
+            const int v = 8 * h + (d & 7);
+            return lds_sum[(w * 8 * G + ((v & ~3) | perm2(v & 3))) * 16 + (d >> 3)];
+        } else {
+            return lds_acc[w][h][d];
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l_run[i] = row16_sum(l_run[i]);
+
     if (lane == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) { lds_m[wave][h] = m_run[h]; lds_l[wave][h] = l_run[h]; }
@@ -554,7 +625,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
 #pragma unroll
         for (int w = 0; w < DEC_WAVES; ++w) {
             const float wt = exp2_fast(lds_m[w][h] - Ms);
-            s = fmaf(wt, lds_acc[w][h][d], s);
+            s = fmaf(wt, acc_at(w, h, d), s);
             L = fmaf(wt, lds_l[w][h], L);
         }
         if (rec == nullptr) {
@@ -593,6 +664,12 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t
     if (a.n_split > 1 && a.ws == nullptr) return hipErrorInvalidValue;
     if (a.b > 65535 || (int64_t)a.n_split * a.hkv > 0x7fffffff) return hipErrorInvalidValue;
     if (a.kv_f32 && a.append) return hipErrorInvalidValue;
+    // the kernel's 32-bit lane offsets: row strides below 2^24 bytes; a ring
+    // of fewer than 2^24 rows spanning less than 2^31 bytes
+    if (a.k_nb1 < 0 || a.k_nb1 >= (1 << 24) || a.v_nb1 < 0 || a.v_nb1 >= (1 << 24)) return hipErrorInvalidValue;
+    if (a.ring_cap > 0 && (a.ring_cap >= (1 << 24) ||
+                           (int64_t)a.ring_cap * (a.k_nb1 > a.v_nb1 ? a.k_nb1 : a.v_nb1) >= ((int64_t)1 << 31)))
+        return hipErrorInvalidValue;
     if (head_dim == 128) {
         if (group == 4) return launch_dg<128, 4>(a, st);
         if (group == 2) return launch_dg<128, 2>(a, st);

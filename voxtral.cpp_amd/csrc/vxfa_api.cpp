@@ -363,6 +363,11 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
         } else if (k->type != VXFA_TYPE_F16) {
             why = "ring: f16 cache only";
             rc = VXFA_UNSUPPORTED;
+        } else if (k->ne[1] >= (1 << 24) ||
+                   (int64_t)k->ne[1] * (int64_t)(k->nb[1] > v->nb[1] ? k->nb[1] : v->nb[1]) >= ((int64_t)1 << 31)) {
+            // the decode kernel reads a ring's rows by 32-bit offsets from its start
+            why = "ring: capacity must be below 2^24 rows and 2 GiB per head slice";
+            rc = VXFA_UNSUPPORTED;
         }
     }
     if (rc != VXFA_OK) {
