@@ -133,7 +133,7 @@ struct DecodeDivs {
     DivMod hkv, split, bgrp, hm, bm;
 };
 
-template <int D, int G, bool QF16, bool MASK, bool KV32>
+template <int D, int G, bool QF16, bool MASK, bool KV32, bool RING>
 __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs dv) {
     static_assert(D == 64 || D == 128, "head dim");
     static_assert(G == 1 || G == 2 || G == 4, "GQA group");
@@ -272,6 +272,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     // ring_cap rows starting at ring_start, (ring_start + pos) mod ring_cap
     // (ring_cap = ring_start = 0 leaves pos unchanged)
     auto row_of = [&](int pos) {
+        if constexpr (!RING) return pos;
         const int r = pos + a.ring_start;
         return r >= a.ring_cap ? r - a.ring_cap : r;
     };
@@ -283,36 +284,34 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     // 32-bit lane offset, row * stride + column bytes by one 24-bit
     // multiply-add (the host keeps strides and ring sizes below 2^24 and a
     // ring's span below 2^31 bytes). Positions p0 + x of a tile clamp to its
-    // last live position q; the tile's base row is that of position bp and
-    // lane x reads row bp + min(x, lim). A whole tile (lim = TP - 1, no ring
-    // wrap inside) reads rows bp + x: the lane offsets are the loop-invariant
-    // ones below and every per-row step goes into the scalar base. A tile
-    // that wraps round the ring takes the cache start as its base and
+    // last live position q: the tile's base row is that of position bp and
+    // lane x reads row bp + min(x, lim), two VALU instructions per address.
+    // In a ring (a template parameter, so a linear cache pays nothing for
+    // it) a tile whose rows wrap takes the cache start as its base and
     // absolute rows as offsets.
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
-    const uint32_t koff0 = __umul24((uint32_t)(lane & 15), knb) + kcol * ESZ;
-    const uint32_t voff0 = __umul24((uint32_t)vrow, vnb) + vcol * ESZ;
     auto load_tile = [&](Tile& T, int t) {
         const int p0 = lo + t * TP;
         const int q = min(p0 + TP, hi_main) - 1;
         const int bp = q >= p0 ? p0 : max(q, 0);
         const int lim = q >= p0 ? q - p0 : 0;
         const int rb = row_of(bp);
-        const bool wrap = a.ring_cap > 0 && rb + lim >= a.ring_cap;
-        const bool whole = !wrap && lim == TP - 1;
-        auto row_off = [&](int x, uint32_t nb) {
+        bool wrap = false;
+        if constexpr (RING) wrap = rb + lim >= a.ring_cap;
+        auto row_off = [&](int x, uint32_t nb, int col) {
             const int rel = min(x, lim);
             int r = rel;
-            if (wrap) r = rb + rel >= a.ring_cap ? rb + rel - a.ring_cap : rb + rel;
-            return __umul24((uint32_t)r, nb);
+            if constexpr (RING) {
+                const int ra = rb + rel >= a.ring_cap ? rb + rel - a.ring_cap : rb + rel;
+                r = wrap ? ra : rel;
+            }
+            return __umul24((uint32_t)r, nb) + (uint32_t)col;
         };
         const char* kt = wrap ? kb : kb + (int64_t)rb * a.k_nb1;
         const char* vt = wrap ? vb : vb + (int64_t)rb * a.v_nb1;
 #pragma unroll
         for (int grp = 0; grp < NG; ++grp) {
-            const char* kbase = whole ? kt + (int64_t)(16 * grp) * a.k_nb1 : kt;
-            const uint32_t ko = whole ? koff0 : row_off(16 * grp + (lane & 15), knb) + kcol * ESZ;
-            const char* kp = kbase + ko;
+            const char* kp = kt + row_off(16 * grp + (lane & 15), knb, kcol * ESZ);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if constexpr (KV32) {
@@ -332,9 +331,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
         }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const char* vbase = whole ? vt + (int64_t)(i * RPI) * a.v_nb1 : vt;
-            const uint32_t vo = whole ? voff0 : row_off(vrow + i * RPI, vnb) + vcol * ESZ;
-            const char* vp = vbase + vo;
+            const char* vp = vt + row_off(vrow + i * RPI, vnb, vcol * ESZ);
             if constexpr (KV32) {
                 T.v[i][0] = *(const floatx4*)(vp);
                 T.v[i][1] = *(const floatx4*)(vp + 16);
@@ -643,11 +640,17 @@ static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
     const DecodeDivs dv = {DivMod::make(a.hkv), DivMod::make(a.n_split), DivMod::make(a.b / a.bk),
                            DivMod::make(a.hm > 0 ? a.hm : 1), DivMod::make(a.bm > 0 ? a.bm : 1)};
     if (a.mask) {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32>), grid, block, 0, st, a, dv);
-        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32>), grid, block, 0, st, a, dv);
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32, false>), grid, block, 0, st, a, dv);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32, false>), grid, block, 0, st, a, dv);
+    } else if (a.ring_cap > 0) {
+        // a ring: f16 cache, no mask tensor (the host rejects anything else)
+        if constexpr (!KV32) {
+            if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, false, true>), grid, block, 0, st, a, dv);
+            else hipLaunchKernelGGL((fa_decode<D, G, false, false, false, true>), grid, block, 0, st, a, dv);
+        }
     } else {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32>), grid, block, 0, st, a, dv);
-        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32>), grid, block, 0, st, a, dv);
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32, false>), grid, block, 0, st, a, dv);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32, false>), grid, block, 0, st, a, dv);
     }
     if (a.n_split > 1)
         hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G * (D / 32), a.b), dim3(64), 0, st, a);
@@ -664,6 +667,7 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t
     if (a.n_split > 1 && a.ws == nullptr) return hipErrorInvalidValue;
     if (a.b > 65535 || (int64_t)a.n_split * a.hkv > 0x7fffffff) return hipErrorInvalidValue;
     if (a.kv_f32 && a.append) return hipErrorInvalidValue;
+    if (a.ring_cap > 0 && (a.kv_f32 || a.mask)) return hipErrorInvalidValue;
     // the kernel's 32-bit lane offsets: row strides below 2^24 bytes; a ring
     // of fewer than 2^24 rows spanning less than 2^31 bytes
     if (a.k_nb1 < 0 || a.k_nb1 >= (1 << 24) || a.v_nb1 < 0 || a.v_nb1 >= (1 << 24)) return hipErrorInvalidValue;
