@@ -150,24 +150,35 @@ def mask_words_expected(sh: Shape, mplane_entry, T, j):
     return out
 
 
+def mask_tile(sh: Shape, plane_off, T):
+    """The kernel's mtile: tile T's first mask row rounded down to 16 bytes
+    (the scalar base) and that row's offset from it."""
+    t0 = plane_off + 32 * T * sh.m_nb1
+    return t0 - (t0 & 15), t0 & 15
+
+
 def mask_words_kernel(sh: Shape, buf, plane_off, T, j, plant=None):
     """The kernel's mw_issue + mw_finish, lane by lane, on the mask bytes:
-    checks every chunk address and returns the extracted words."""
+    32-bit offsets from the tile's 16-byte-aligned base; checks every chunk
+    address and returns the extracted words."""
     out = np.zeros((64, 2, 8), dtype=np.uint32)
+    base16, d0 = mask_tile(sh, plane_off, T)
     for lane in range(64):
         nl, hh = lane & 31, lane >> 5
         row = 32 * T + nl
-        rowp = plane_off + (row if row < sh.nq else 0) * sh.m_nb1
-        last = (rowp + 2 * sh.nkv - 1) & ~15
+        rs = d0 + (nl if row < sh.nq else 0) * sh.m_nb1
+        _check(0 <= rs < 2**31, "mask row offset beyond 32 bits")
+        rowp = base16 + rs
+        last = (rs + 2 * sh.nkv - 1) & ~15
         for kvb in range(2):
-            seg = rowp + 2 * (TK * j + 32 * kvb + 16 * hh)
-            s = seg & 15
-            pa = seg - s
-            lim = last - pa
+            segr = rs + 2 * (TK * j + 32 * kvb + 16 * hh)
+            s = segr & 15
+            pr = segr & ~15
+            lim = last - pr
             chunks = []
             for i in range(3):
                 off = 16 * i if plant == "no_chunk_clamp" else min(16 * i, lim)
-                a = pa + off
+                a = base16 + pr + off
                 _check(a % 16 == 0, f"mask chunk not 16-byte aligned: {a}")
                 # the granule [a, a + 16) must hold a byte of the row's data
                 _check(a < rowp + 2 * sh.nkv and a + 16 > rowp,
@@ -204,17 +215,19 @@ def classify_kernel(sh: Shape, buf, plane_off, T, j, plant=None):
     segment read as 16-byte-aligned chunks, nine lanes per row, seven rows per
     load, five loads; checks every chunk address, returns the class."""
     live = nonzero = False
+    base16, d0 = mask_tile(sh, plane_off, T)
     for u in range(5):
         for lane in range(64):
             lr, lc = lane // 9, lane % 9
-            row = 32 * T + 7 * u + lr
-            ok = lr < 7 and 7 * u + lr < 32 and row < sh.nq
-            rowp = plane_off + (row if ok else 0) * sh.m_nb1
-            last = (rowp + 2 * sh.nkv - 1) & ~15
-            seg = rowp + 2 * TK * j
-            pa = seg - (seg & 15)
-            lim = last - pa
-            a = pa + (16 * lc if plant == "no_chunk_clamp" else min(16 * lc, lim))
+            rr = 7 * u + lr
+            ok = lr < 7 and rr < 32 and 32 * T + rr < sh.nq
+            rs = d0 + (rr * sh.m_nb1 if ok else 0)
+            _check(0 <= rs < 2**31, "mask row offset beyond 32 bits")
+            rowp = base16 + rs
+            last = (rs + 2 * sh.nkv - 1) & ~15
+            pr = (rs + 2 * TK * j) & ~15
+            lim = last - pr
+            a = base16 + pr + (16 * lc if plant == "no_chunk_clamp" else min(16 * lc, lim))
             _check(a % 16 == 0, "classification chunk not 16-byte aligned")
             _check(a < rowp + 2 * sh.nkv and a + 16 > rowp,
                    f"classification chunk {a} outside row data [{rowp}, {rowp + 2 * sh.nkv})")
@@ -222,9 +235,9 @@ def classify_kernel(sh: Shape, buf, plane_off, T, j, plant=None):
             n = max(0, min(16, len(buf) - a))
             c[:n] = buf[a:a + n]
             w16 = c.view(np.uint16)
-            e0 = (pa + 16 * lc - rowp) // 2
+            e0 = (pr - rs + 16 * lc) // 2 if ok else 1 << 20
             lo, hi = max(TK * j - e0, 0), min(min(TK * j + TK, sh.nkv) - e0, 8)
-            if not ok or hi <= lo:
+            if hi <= lo:
                 continue
             for k in range(lo, hi):
                 v = int(w16[k])

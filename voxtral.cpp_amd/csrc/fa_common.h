@@ -403,6 +403,8 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t stream);
 // masked hd 128 prefill with n_kv <= 512 (a mask tensor or an implicit mask;
 // a rotary embedding of F32 Q)
 hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t stream);
+// whether launch_prefill_pair takes these strides (its 32-bit offsets)
+bool prefill_pair_fits(const AttnArgs& a);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
 // F32 -> f16 copy of a [D, n, H, B] view (byte strides nb1..nb3, rows

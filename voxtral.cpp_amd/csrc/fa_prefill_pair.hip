@@ -71,7 +71,8 @@ __device__ __forceinline__ void pr_lds_barrier() {
 }
 
 template <int MM, bool QF16>   // MM 1: mask tensor, 2: implicit mask
-__global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm, int nt, int nk) {
+__global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm, DivMod hmd, DivMod bmd, int nt,
+                                                           int nk) {
     using namespace pr;
     static_assert(MM == 1 || MM == 2, "masked calls only");
     __shared__ __attribute__((aligned(16))) char sV[MAXK * VT];   // V tiles; then the published O
@@ -98,35 +99,52 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     // Lane half 0 holds positions 0..15 of each 32-block in order, half 1
     // positions 16..31 with its two 8-position halves swapped (the row-to-KV
     // permutation). Positions past n_kv and rows past n_q read -inf.
+    // Mask rows of query tile T are addressed from a 16-byte-aligned scalar
+    // base (the tile's first row rounded down) by 32-bit offsets: row rr of
+    // the tile starts rs = d0 + rr * m_nb1 bytes after it (the host keeps
+    // n_q * m_nb1 below 2^31 and m_nb1 below 2^24). Rows past n_q read the
+    // tile's first row (their entries are dropped).
     const char* mplane = nullptr;
     if constexpr (MM == 1)
-        mplane = (const char*)a.mask + (int64_t)(h % a.hm) * a.m_nb2 + (int64_t)(b % a.bm) * a.m_nb3;
+        mplane = (const char*)a.mask + (int64_t)hmd.mod((uint32_t)h) * a.m_nb2 + (int64_t)bmd.mod((uint32_t)b) * a.m_nb3;
+    const uint32_t mnb = (uint32_t)a.m_nb1;
+    const uint32_t rowbytes = 2u * (uint32_t)a.nkv;   // bytes of mask data per row
+    auto mtile = [&](int T, uint32_t& d0) -> const char* {
+        const uintptr_t t0 = reinterpret_cast<uintptr_t>(mplane) + (uintptr_t)(32 * T) * (uintptr_t)a.m_nb1;
+        d0 = (uint32_t)(t0 & 15);
+        return reinterpret_cast<const char*>(t0 - d0);
+    };
     // Tensor: the lane's 16 entries of a 32-block are 32 bytes at any 2-byte
     // alignment (voxtral's n x n rows are 2n bytes apart), read as the three
     // 16-byte-aligned chunks that cover them. A chunk past the row's last data
     // granule is replaced by that granule, so every chunk read holds mask data
     // of the row (same allocation, same page); entries taken from it lie past
     // n_kv and are replaced by -inf.
+    auto mw_rs = [&](int T, uint32_t d0) {   // start of the lane's row, from the tile base
+        const int rr = 32 * T + nl < a.nq ? nl : 0;
+        return d0 + __umul24((uint32_t)rr, mnb);
+    };
     auto mw_issue = [&](int T, int j, u32x4 (&ch)[2][3]) {
-        const int row = 32 * T + nl;
-        const char* rowp = mplane + (int64_t)(row < a.nq ? row : 0) * a.m_nb1;
-        const uintptr_t last = (reinterpret_cast<uintptr_t>(rowp) + 2 * (uintptr_t)a.nkv - 1) & ~(uintptr_t)15;
+        uint32_t d0;
+        const char* mb = mtile(T, d0);
+        const uint32_t rs = mw_rs(T, d0);
+        const uint32_t last = (rs + rowbytes - 1u) & ~15u;
 #pragma unroll
         for (int kvb = 0; kvb < 2; ++kvb) {
-            const char* seg = rowp + 2 * (TK * j + 32 * kvb + 16 * hh);
-            const int sh = (int)(reinterpret_cast<uintptr_t>(seg) & 15);
-            const char* pa = seg - sh;
-            const int lim = (int)((intptr_t)last - (intptr_t)reinterpret_cast<uintptr_t>(pa));   // multiple of 16
+            const uint32_t pa = (rs + 2u * (uint32_t)(TK * j + 32 * kvb + 16 * hh)) & ~15u;
+            const int lim = (int)(last - pa);   // a multiple of 16
 #pragma unroll
-            for (int i = 0; i < 3; ++i) ch[kvb][i] = *(const u32x4*)(pa + min(16 * i, lim));
+            for (int i = 0; i < 3; ++i) ch[kvb][i] = *(const u32x4*)(mb + (pa + (uint32_t)min(16 * i, lim)));
         }
     };
     auto mw_finish = [&](int T, int j, const u32x4 (&ch)[2][3], uint32_t (&mw)[2][8]) {
         const int row = 32 * T + nl;
-        const char* rowp = mplane + (int64_t)(row < a.nq ? row : 0) * a.m_nb1;
+        uint32_t d0;
+        (void)mtile(T, d0);
+        const uint32_t rs = mw_rs(T, d0);
 #pragma unroll
         for (int kvb = 0; kvb < 2; ++kvb) {
-            const int sh = (int)(reinterpret_cast<uintptr_t>(rowp + 2 * (TK * j + 32 * kvb + 16 * hh)) & 15);
+            const int sh = (int)((rs + 2u * (uint32_t)(TK * j + 32 * kvb + 16 * hh)) & 15u);
             const int q4 = sh >> 2, s2 = sh & 2;
             uint32_t d[12];
 #pragma unroll
@@ -198,19 +216,22 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     constexpr int QPT = 2 * 32 * QCH / NT;        // per thread
     floatx4 qraw[QPT];
     int qpos[QPT];   // rotary position of the chunk's row (F32 Q)
+    // (rows from a scalar base by 32-bit offsets: the host keeps n_q * q_nb1
+    // below 2^31 and q_nb1 below 2^24)
+    const char* qhb = (const char*)a.q + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
+    const int* qpb = a.rope_pos ? a.rope_pos + (int64_t)b * a.nq : (const int*)a.q;
     auto issue_q = [&]() {
 #pragma unroll
         for (int u = 0; u < QPT; ++u) {
             const int i = tid + NT * u;
             const int s = i / (32 * QCH), r = (i / QCH) % 32, cch = i % QCH;
             const int row = min(32 * (s ? tB : tA) + r, a.nq - 1);
-            qraw[u] = __builtin_nontemporal_load((const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 +
-                                                                  (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3 + cch * 16));
+            qraw[u] = __builtin_nontemporal_load(
+                (const floatx4*)(qhb + (__umul24((uint32_t)row, (uint32_t)a.q_nb1) + (uint32_t)(cch * 16))));
             if constexpr (!QF16) {
                 // read without a branch: without a rotary embedding it reads
                 // the first word of Q, unused
-                const int* pp = a.rope_pos ? a.rope_pos + ((int64_t)b * a.nq + row) : (const int*)a.q;
-                qpos[u] = *pp;
+                qpos[u] = qpb[(uint32_t)(a.rope_pos ? row : 0)];
             }
         }
     };
@@ -227,31 +248,30 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
         // data granule is replaced by that granule; entries outside the
         // segment, past n_kv or of rows past n_q are dropped in registers.
         const int lr = lane / 9, lc = lane - 9 * (lane / 9);
-        auto cls_issue = [&](int T, int j, u32x4 (&cw)[5]) {
+        // e0[u]: entry index (in the row) of the lane's chunk's first entry,
+        // or a large value for a lane without a row (no entry is taken)
+        auto cls_issue = [&](int T, int j, u32x4 (&cw)[5], int (&e0)[5]) {
+            uint32_t d0;
+            const char* mb = mtile(T, d0);
 #pragma unroll
             for (int u = 0; u < 5; ++u) {
-                const int row = 32 * T + 7 * u + lr;
-                const bool ok = lr < 7 && 7 * u + lr < 32 && row < a.nq;
-                const char* rowp = mplane + (int64_t)(ok ? row : 0) * a.m_nb1;
-                const uintptr_t last = (reinterpret_cast<uintptr_t>(rowp) + 2 * (uintptr_t)a.nkv - 1) & ~(uintptr_t)15;
-                const char* seg = rowp + 2 * TK * j;
-                const char* pa = seg - (int)(reinterpret_cast<uintptr_t>(seg) & 15);
-                const int lim = (int)((intptr_t)last - (intptr_t)reinterpret_cast<uintptr_t>(pa));
-                cw[u] = *(const u32x4*)(pa + min(16 * lc, lim));
+                const int rr = 7 * u + lr;
+                const bool ok = lr < 7 && rr < 32 && 32 * T + rr < a.nq;
+                const uint32_t rs = d0 + (ok ? __umul24((uint32_t)rr, mnb) : 0u);
+                const uint32_t last = (rs + rowbytes - 1u) & ~15u;
+                const uint32_t pa = (rs + 2u * TK * (uint32_t)j) & ~15u;
+                const int lim = (int)(last - pa);
+                cw[u] = *(const u32x4*)(mb + (pa + (uint32_t)min(16 * lc, lim)));
+                e0[u] = ok ? ((int)(pa - rs) + 16 * lc) / 2 : (1 << 20);
             }
         };
-        auto cls_eval = [&](int T, int j, const u32x4 (&cw)[5]) -> int {
+        auto cls_eval = [&](int j, const u32x4 (&cw)[5], const int (&e0)[5]) -> int {
             bool live = false, nonzero = false;
 #pragma unroll
             for (int u = 0; u < 5; ++u) {
-                const int row = 32 * T + 7 * u + lr;
-                const bool ok = lr < 7 && 7 * u + lr < 32 && row < a.nq;
-                const char* rowp = mplane + (int64_t)(ok ? row : 0) * a.m_nb1;
-                const char* seg = rowp + 2 * TK * j;
-                const int e0 = (int)((seg - (int)(reinterpret_cast<uintptr_t>(seg) & 15) + 16 * lc) - rowp) / 2;
                 // entries k of the chunk inside [64 j, min(64 j + 64, n_kv))
-                const int lo = max(TK * j - e0, 0), hi = min(min(TK * j + TK, a.nkv) - e0, 8);
-                const uint32_t m8 = (ok && hi > lo) ? (((1u << hi) - 1u) & ~((1u << lo) - 1u)) : 0u;
+                const int lo = max(TK * j - e0[u], 0), hi = min(min(TK * j + TK, a.nkv) - e0[u], 8);
+                const uint32_t m8 = hi > lo ? (((1u << hi) - 1u) & ~((1u << lo) - 1u)) : 0u;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
                     const uint32_t wm = (((m8 >> (2 * w)) & 1u) ? 0x0000FFFFu : 0u) |
@@ -265,11 +285,12 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
             return !any_live ? 0 : (__any(nonzero) || TK * j + TK > a.nkv) ? 3 : 1;
         };
         u32x4 cwB[5], cwA[5];
+        int e0B[5], e0A[5];
         // (a candidate that does not exist reads tile B's or A's first block)
-        cls_issue(tB, candB ? jB : 0, cwB);
-        cls_issue(tA, candA ? jA : 0, cwA);
+        cls_issue(tB, candB ? jB : 0, cwB, e0B);
+        cls_issue(tA, candA ? jA : 0, cwA, e0A);
         issue_q();   // after the mask loads: their wait does not include Q's
-        const int cB = cls_eval(tB, candB ? jB : 0, cwB), cA = cls_eval(tA, candA ? jA : 0, cwA);
+        const int cB = cls_eval(candB ? jB : 0, cwB, e0B), cA = cls_eval(candA ? jA : 0, cwA, e0A);
         if (lane == 0) {
             if (candB) s_cls[MAXK + jB] = (uint8_t)cB;
             if (candA) s_cls[jA] = (uint8_t)cA;
@@ -577,6 +598,16 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
 
 // Short masked prefill: hd 128, a mask tensor or an implicit mask, n_kv <= 512
 // (a rotary embedding of F32 Q applied as it is staged).
+// The 32-bit offsets of the kernel: Q and mask rows from a per-tile base
+// (row strides below 2^24 bytes, n_q rows below 2^31 bytes).
+bool prefill_pair_fits(const AttnArgs& a) {
+    const int64_t lim = (int64_t)1 << 31, s24 = (int64_t)1 << 24;
+    if (a.nq <= 0 || a.nq >= (1 << 24)) return false;
+    if (a.q_nb1 < 0 || a.q_nb1 >= s24 || (int64_t)a.nq * a.q_nb1 >= lim) return false;
+    if (a.mask && (a.m_nb1 < 0 || a.m_nb1 >= s24 || ((int64_t)a.nq + 32) * a.m_nb1 >= lim)) return false;
+    return true;
+}
+
 hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t st) {
     using namespace pr;
     if (!(a.mask != nullptr || a.im_causal) || (a.rope_pos != nullptr && a.q_f16)) return hipErrorInvalidValue;
@@ -586,14 +617,16 @@ hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t st) {
     const int np = (nt + 1) / 2;
     const int64_t nwg = (int64_t)np * a.hq * a.b;
     if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
+    if (!prefill_pair_fits(a)) return hipErrorInvalidValue;
     const GridMap gm = GridMap::make((int)nwg, np, a.hq, a.hkv, a.b, a.bk);
+    const DivMod hmd = DivMod::make(a.hm > 0 ? a.hm : 1), bmd = DivMod::make(a.bm > 0 ? a.bm : 1);
     const dim3 grid((unsigned)nwg), block(NT);
     if (a.im_causal) {
-        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<2, true>), grid, block, 0, st, a, gm, nt, nk);
-        else hipLaunchKernelGGL((fa_prefill_pair<2, false>), grid, block, 0, st, a, gm, nt, nk);
+        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<2, true>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
+        else hipLaunchKernelGGL((fa_prefill_pair<2, false>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
     } else {
-        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<1, true>), grid, block, 0, st, a, gm, nt, nk);
-        else hipLaunchKernelGGL((fa_prefill_pair<1, false>), grid, block, 0, st, a, gm, nt, nk);
+        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<1, true>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
+        else hipLaunchKernelGGL((fa_prefill_pair<1, false>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
     }
     return hipGetLastError();
 }

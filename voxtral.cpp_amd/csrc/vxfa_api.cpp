@@ -510,7 +510,7 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel
             e = vxfa::launch_prefill64_pp(a, st);
-        } else if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled) {
+        } else if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled && vxfa::prefill_pair_fits(a)) {
             // short masked prefill (voxtral's decoder prefill): paired query
             // tiles, every live block on its own wavefront
             e = vxfa::launch_prefill_pair(a, st);
