@@ -149,15 +149,32 @@ struct AppendArgs {
 // cos / sin of pair j's angle at position p (see rope8 below): the running
 // product to pair j, reduced modulo 2 pi in double precision (error ~1e-12)
 // so sincosf takes its short-argument path, rounded to float.
-__device__ __forceinline__ float2 rope_cs(int p, int j, float ts) {
-    float th = (float)p;
-    for (int i = 0; i < j; ++i) th *= ts;
+__device__ __forceinline__ float2 rope_cs_of_angle(float th) {
     const double td = (double)th;
     const double kq = __builtin_rint(td * 0.15915494309189535);
     const float r = (float)__builtin_fma(-kq, 6.283185307179586, td);
     float s, c;
     sincosf(r, &s, &c);
     return float2{c, s};
+}
+__device__ __forceinline__ float2 rope_cs(int p, int j, float ts) {
+    float th = (float)p;
+    for (int i = 0; i < j; ++i) th *= ts;
+    return rope_cs_of_angle(th);
+}
+// rope_cs for pair j < NP of one position p shared by the calling lanes: every
+// lane runs the same NP - 1 step running product (fully unrolled, two VALU
+// instructions a step) and keeps step j, instead of a loop whose trip count
+// differs per lane (~6 instructions an iteration, up to NP - 1 iterations).
+template <int NP>
+__device__ __forceinline__ float2 rope_cs_chain(int p, int j, float ts) {
+    float th = (float)p, mine = th;
+#pragma unroll
+    for (int i = 1; i < NP; ++i) {
+        th *= ts;
+        mine = j == i ? th : mine;
+    }
+    return rope_cs_of_angle(mine);
 }
 
 // rope8 with the pairs' cos / sin taken from a table: cs[j] = rope_cs(p, j, ts).

@@ -376,7 +376,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     // asm takes the position as an operand after those loads are issued, so
     // the wait for it stays below them.)
     asm volatile("" : "+v"(rope_p) : : "memory");
-    if (a.rope_pos && tid < D / 2) lds_rope[tid] = rope_cs(rope_p, tid, a.rope_ts);
+    if (a.rope_pos && tid < D / 2) lds_rope[tid] = rope_cs_chain<D / 2>(rope_p, tid, a.rope_ts);
     if (q_loader) {
         half8 qh8;
         if constexpr (QF16) {
