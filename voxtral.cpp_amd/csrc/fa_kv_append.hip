@@ -22,7 +22,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
     __shared__ float2 cs[128];
     if (a.rope_pos) {
         const int p = a.rope_pos[b * a.n_new + t];
-        for (int j = threadIdx.x; j < a.d / 2; j += 256) cs[j] = rope_cs(p, j, a.rope_ts);
+        // (pairs below 64: one unrolled running product shared by the lanes)
+        for (int j = threadIdx.x; j < a.d / 2; j += 256)
+            cs[j] = j < 64 ? rope_cs_chain<64>(p, j, a.rope_ts) : rope_cs(p, j, a.rope_ts);
         __syncthreads();
     }
     for (int c = threadIdx.x; c < 2 * per; c += 256) {

@@ -215,7 +215,7 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     constexpr int QCH = QF16 ? 16 : 32;           // 16-byte global chunks per row
     constexpr int QPT = 2 * 32 * QCH / NT;        // per thread
     floatx4 qraw[QPT];
-    int qpos[QPT];   // rotary position of the chunk's row (F32 Q)
+    int rowpos = 0;   // rotary position of staged row `lane` (0-31 tile A, 32-63 tile B; F32 Q)
     // (rows from a scalar base by 32-bit offsets: the host keeps n_q * q_nb1
     // below 2^31 and q_nb1 below 2^24)
     const char* qhb = (const char*)a.q + (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3;
@@ -228,11 +228,12 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
             const int row = min(32 * (s ? tB : tA) + r, a.nq - 1);
             qraw[u] = __builtin_nontemporal_load(
                 (const floatx4*)(qhb + (__umul24((uint32_t)row, (uint32_t)a.q_nb1) + (uint32_t)(cch * 16))));
-            if constexpr (!QF16) {
-                // read without a branch: without a rotary embedding it reads
-                // the first word of Q, unused
-                qpos[u] = qpb[(uint32_t)(a.rope_pos ? row : 0)];
-            }
+        }
+        if constexpr (!QF16) {
+            // read without a branch: without a rotary embedding it reads the
+            // first word of Q, unused
+            const int rrow = min(32 * (lane >= 32 ? tB : tA) + (lane & 31), a.nq - 1);
+            rowpos = qpb[(uint32_t)(a.rope_pos ? rrow : 0)];
         }
     };
 
@@ -394,6 +395,42 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
         if (mix0) mw_finish(T, j0, chr0, mw0);
         if (mix1) mw_finish(T, j1, chr1, mw1);
     }
+    // Rotary angles (F32 Q with rope_pos): the angle of pair j of staged row
+    // R (0-31 tile A, 32-63 tile B) in a table over the Q area, at float
+    // R * 64 + (j ^ R) (the XOR spreads the writes, one pair of every row,
+    // and the reads, two pairs of one row, over the banks). Wavefront 0 forms
+    // each row's running product once (lane = row), as ggml builds its
+    // cos / sin cache, and every lane takes the cos / sin of its chunk's two
+    // pairs from it (a per-lane product loop cost ~6 instructions per step
+    // for up to 62 steps per chunk).
+    float2 qcs[QPT][2];
+    if constexpr (!QF16) {
+        if (a.rope_pos) {
+            float* tab = reinterpret_cast<float*>(sQ);
+            static_assert(64 * (D / 2) * sizeof(float) <= 2 * QT, "angle table fits the Q area");
+            if (wave == 0) {
+                float th = (float)rowpos;
+#pragma unroll
+                for (int j = 0; j < D / 2; ++j) {
+                    tab[lane * 64 + (j ^ lane)] = th;
+                    th *= a.rope_ts;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < QPT; ++u) {
+                const int i = tid + NT * u;
+                const int s = i / (32 * QCH), r = (i / QCH) % 32, cch = i % QCH;
+                const int R = 32 * s + r;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int j = 2 * cch + k;
+                    qcs[u][k] = rope_cs_of_angle(tab[R * 64 + (j ^ R)]);
+                }
+            }
+            __syncthreads();   // every angle read before the rows overwrite the table
+        }
+    }
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         const int i = tid + NT * u;
@@ -407,7 +444,17 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
             // rotated first when a rotary embedding is given (ggml rotates
             // Q before the attention node)
             float xr[4] = {x[0], x[1], x[2], x[3]};
-            if (a.rope_pos) rope_n<4>(xr, qpos[u], 4 * cch, a.rope_ts, a.rope_dims);
+            if (a.rope_pos) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    if (4 * cch + 2 * k < a.rope_dims) {
+                        const float cs_ = qcs[u][k].x, sn = qcs[u][k].y;
+                        const float x0 = xr[2 * k], x1 = xr[2 * k + 1];
+                        xr[2 * k] = x0 * cs_ - x1 * sn;
+                        xr[2 * k + 1] = x0 * sn + x1 * cs_;
+                    }
+                }
+            }
             half4 v;
 #pragma unroll
             for (int e2 = 0; e2 < 4; ++e2) v[e2] = (_Float16)xr[e2];
