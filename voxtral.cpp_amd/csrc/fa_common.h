@@ -214,6 +214,19 @@ __device__ __forceinline__ void rope_n(float (&x)[N], int p, int d0, float ts, i
     }
 }
 
+// rope8 with the four pairs' angles given (d0 / 2 .. d0 / 2 + 3)
+__device__ __forceinline__ void rope8_ang(float (&x)[8], const float (&ang)[4], int d0, int n_dims) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (d0 + 2 * k < n_dims) {
+            const float2 cs = rope_cs_of_angle(ang[k]);
+            const float x0 = x[2 * k], x1 = x[2 * k + 1];
+            x[2 * k] = x0 * cs.x - x1 * cs.y;
+            x[2 * k + 1] = x0 * cs.y + x1 * cs.x;
+        }
+    }
+}
+
 __device__ __forceinline__ void rope8(float (&x)[8], int p, int d0, float ts, int n_dims) {
     rope_n<8>(x, p, d0, ts, n_dims);
 }

@@ -332,13 +332,26 @@ __global__ __launch_bounds__(64 * NQW * KVG) void fa_prefill_kernel(AttnArgs a, 
     }
     // rounds the F32 rows to f16 (ggml's Q conversion), rotating them first
     // when a rotary embedding is given; zeroes rows past n_q
+    // (The rotation's angles come from one running product over the row's
+    // pairs, as ggml builds its cos / sin cache: pair 8 ks + o, o < 8, belongs
+    // to the lanes with hh = o / 4, which keep it for their slot o % 4; a
+    // product loop restarted for every ks cost ~6 instructions per step.)
     auto finish_q = [&]() {
         if constexpr (!QF16) {
+            float th = (float)qpos;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8] = {qraw[ks][0][0], qraw[ks][0][1], qraw[ks][0][2], qraw[ks][0][3],
                               qraw[ks][1][0], qraw[ks][1][1], qraw[ks][1][2], qraw[ks][1][3]};
-                if (a.rope_pos) rope8(x, qpos, 16 * ks + 8 * hh, a.rope_ts, a.rope_dims);
+                if (a.rope_pos) {
+                    float ang[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int o = 0; o < 8; ++o) {
+                        if (ks > 0 || o > 0) th *= a.rope_ts;
+                        if ((o >> 2) == hh) ang[o & 3] = th;
+                    }
+                    rope8_ang(x, ang, 16 * ks + 8 * hh, a.rope_dims);
+                }
 #pragma unroll
                 for (int e = 0; e < 8; ++e) qb[ks][e] = (_Float16)x[e];
             }
