@@ -142,21 +142,42 @@ struct AppendArgs {
 // x[2j+1]) of a head turns by theta_j, where theta_0 = p and each next
 // pair's angle is the previous one times ts = freq_base^(-2 / n_dims), in
 // that order (ggml builds its cos/sin cache by this running product), and
-// x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos. x holds dims d0 .. d0 + 7
-// (d0 even); dims at or past n_dims are left as they are. cos and sin are
-// taken of the angle reduced modulo 2 pi in double precision and rounded to
-// float (within a float ulp of the unreduced angle's cosf / sinf).
-// cos / sin of pair j's angle at position p (see rope8 below): the running
-// product to pair j, reduced modulo 2 pi in double precision (error ~1e-12)
-// so sincosf takes its short-argument path, rounded to float.
+// x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos; dims at or past n_dims are
+// left as they are.
+//
+// (cos, sin) of a float angle: reduced by the nearest multiple q of pi / 2 in
+// double precision (error ~1e-12 at the angles rotary embeddings reach), sin
+// and cos of the remainder r (|r| <= pi / 4) by their Taylor series through
+// r^11 and r^12 (truncation below 1e-11, float rounding a few ulp), then the
+// quadrant q mod 4 swaps and negates them. Straight-line code: the library's
+// sincosf carries a large-argument path whose code, repeated for every pair a
+// lane rotates, cost more than the arithmetic.
 __device__ __forceinline__ float2 rope_cs_of_angle(float th) {
     const double td = (double)th;
-    const double kq = __builtin_rint(td * 0.15915494309189535);
-    const float r = (float)__builtin_fma(-kq, 6.283185307179586, td);
-    float s, c;
-    sincosf(r, &s, &c);
-    return float2{c, s};
+    const double qd = __builtin_rint(td * 0.63661977236758134);   // 2 / pi
+    const float r = (float)__builtin_fma(-qd, 1.5707963267948966, td);
+    const int q = (int)(long long)qd & 3;
+    const float r2 = r * r;
+    float sn = -2.5052108385e-8f;            // -1/11!
+    sn = fmaf(sn, r2, 2.7557319224e-6f);      //  1/9!
+    sn = fmaf(sn, r2, -1.9841269841e-4f);     // -1/7!
+    sn = fmaf(sn, r2, 8.3333333333e-3f);      //  1/5!
+    sn = fmaf(sn, r2, -1.6666666667e-1f);     // -1/3!
+    sn = fmaf(sn * r2, r, r);
+    float cs = 2.0876756988e-9f;              //  1/12!
+    cs = fmaf(cs, r2, -2.7557319224e-7f);     // -1/10!
+    cs = fmaf(cs, r2, 2.4801587302e-5f);      //  1/8!
+    cs = fmaf(cs, r2, -1.3888888889e-3f);     // -1/6!
+    cs = fmaf(cs, r2, 4.1666666667e-2f);      //  1/4!
+    cs = fmaf(cs, r2, -0.5f);
+    cs = fmaf(cs, r2, 1.0f);
+    // angle = q pi / 2 + r: q = 1 gives (-sin r, cos r), 2 (-cos r, -sin r),
+    // 3 (sin r, -cos r)
+    const float cq = (q & 1) ? sn : cs;
+    const float sq = (q & 1) ? cs : sn;
+    return float2{(q == 1 || q == 2) ? -cq : cq, (q & 2) ? -sq : sq};
 }
+// cos / sin of pair j's angle at position p: the running product to pair j
 __device__ __forceinline__ float2 rope_cs(int p, int j, float ts) {
     float th = (float)p;
     for (int i = 0; i < j; ++i) th *= ts;
@@ -177,7 +198,8 @@ __device__ __forceinline__ float2 rope_cs_chain(int p, int j, float ts) {
     return rope_cs_of_angle(mine);
 }
 
-// rope8 with the pairs' cos / sin taken from a table: cs[j] = rope_cs(p, j, ts).
+// x holds dims d0 .. d0 + 7 (d0 even), the pairs' cos / sin taken from a table:
+// cs[j] = rope_cs(p, j, ts).
 __device__ __forceinline__ void rope8_tab(float (&x)[8], int d0, const float2* cs, int n_dims) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -190,31 +212,8 @@ __device__ __forceinline__ void rope8_tab(float (&x)[8], int d0, const float2* c
     }
 }
 
-// dims d0 .. d0 + N - 1 (N = 4 or 8); rope8 = rope_n<8>
-template <int N>
-__device__ __forceinline__ void rope_n(float (&x)[N], int p, int d0, float ts, int n_dims) {
-    if (d0 >= n_dims) return;
-    float th = (float)p;
-    for (int j = 0; j < d0 / 2; ++j) th *= ts;   // the running product up to pair d0 / 2
-#pragma unroll
-    for (int k = 0; k < N / 2; ++k) {
-        if (d0 + 2 * k < n_dims) {
-            // angles reach n_ctx radians: reduce by 2 pi in double first (error
-            // ~1e-12), then sincosf's short-argument path applies
-            const double td = (double)th;
-            const double kq = __builtin_rint(td * 0.15915494309189535);
-            const float r = (float)__builtin_fma(-kq, 6.283185307179586, td);
-            float s, c;
-            sincosf(r, &s, &c);
-            const float x0 = x[2 * k], x1 = x[2 * k + 1];
-            x[2 * k] = x0 * c - x1 * s;
-            x[2 * k + 1] = x0 * s + x1 * c;
-        }
-        th *= ts;
-    }
-}
-
-// rope8 with the four pairs' angles given (d0 / 2 .. d0 / 2 + 3)
+// x holds dims d0 .. d0 + 7 (d0 even), the four pairs' angles given (pairs
+// d0 / 2 .. d0 / 2 + 3)
 __device__ __forceinline__ void rope8_ang(float (&x)[8], const float (&ang)[4], int d0, int n_dims) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -225,10 +224,6 @@ __device__ __forceinline__ void rope8_ang(float (&x)[8], const float (&ang)[4], 
             x[2 * k + 1] = x0 * cs.y + x1 * cs.x;
         }
     }
-}
-
-__device__ __forceinline__ void rope8(float (&x)[8], int p, int d0, float ts, int n_dims) {
-    rope_n<8>(x, p, d0, ts, n_dims);
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
