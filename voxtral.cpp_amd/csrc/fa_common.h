@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace vxfa {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -300,41 +302,46 @@ __device__ __forceinline__ void mask_live_range(const uint16_t* base, int64_t ro
     const int items = rows * ncr;
     constexpr uint32_t DEAD = 0xFC00FC00u;
     int tlo = 0x7fffffff, thi = -1;
-    for (int i0 = tid; i0 < items; i0 += U * NT) {
-        u32x4 w[U];
-        int col[U];   // row column of the chunk's first entry (may be < 0); n when unused
+    // (one row, the common case: chunk i is column chunk i, no division)
+    auto scan = [&](auto one_row) {
+        for (int i0 = tid; i0 < items; i0 += U * NT) {
+            u32x4 w[U];
+            int col[U];   // row column of the chunk's first entry (may be < 0); n when unused
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = i0 + u * NT;
-            const int r = i / ncr, c = i - r * ncr;
-            const char* rowp = reinterpret_cast<const char*>(base) + (int64_t)r * row_stride;
-            const int off = 16 * c - (int)(reinterpret_cast<uintptr_t>(rowp) & 15);   // bytes from the row start
-            const bool ok = i < items && off < 2 * n;
-            col[u] = ok ? off / 2 : n;
-            w[u] = u32x4{DEAD, DEAD, DEAD, DEAD};
-            if (ok) w[u] = *reinterpret_cast<const u32x4*>(rowp + off);
+            for (int u = 0; u < U; ++u) {
+                const int i = i0 + u * NT;
+                const int r = decltype(one_row)::value ? 0 : i / ncr, c = i - r * ncr;
+                const char* rowp = reinterpret_cast<const char*>(base) + (int64_t)r * row_stride;
+                const int off = 16 * c - (int)(reinterpret_cast<uintptr_t>(rowp) & 15);   // bytes from the row start
+                const bool ok = i < items && off < 2 * n;
+                col[u] = ok ? off / 2 : n;
+                w[u] = u32x4{DEAD, DEAD, DEAD, DEAD};
+                if (ok) w[u] = *reinterpret_cast<const u32x4*>(rowp + off);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if ((w[u][0] & w[u][1]) == DEAD && (w[u][2] & w[u][3]) == DEAD &&
+                    (w[u][0] | w[u][1] | w[u][2] | w[u][3]) == DEAD)
+                    continue;   // eight -inf entries
+                uint32_t m = 0;   // bit e: entry e is not -inf
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    m |= ((w[u][j] & 0xFFFFu) != kF16NegInf ? 1u : 0u) << (2 * j);
+                    m |= ((w[u][j] >> 16) != kF16NegInf ? 1u : 0u) << (2 * j + 1);
+                }
+                if (col[u] < 0 || col[u] > n - 8) {   // a chunk reaching outside the row
+                    const int e_lo = min(max(-col[u], 0), 8), e_hi = min(max(n - col[u], 0), 8);
+                    m &= e_hi > e_lo ? ((1u << (e_hi - e_lo)) - 1u) << e_lo : 0u;
+                }
+                if (m) {
+                    tlo = min(tlo, col[u] + (int)__builtin_ctz(m));
+                    thi = max(thi, col[u] + 31 - (int)__builtin_clz(m));
+                }
+            }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if ((w[u][0] & w[u][1]) == DEAD && (w[u][2] & w[u][3]) == DEAD &&
-                (w[u][0] | w[u][1] | w[u][2] | w[u][3]) == DEAD)
-                continue;   // eight -inf entries
-            uint32_t m = 0;   // bit e: entry e is not -inf
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                m |= ((w[u][j] & 0xFFFFu) != kF16NegInf ? 1u : 0u) << (2 * j);
-                m |= ((w[u][j] >> 16) != kF16NegInf ? 1u : 0u) << (2 * j + 1);
-            }
-            if (col[u] < 0 || col[u] > n - 8) {   // a chunk reaching outside the row
-                const int e_lo = min(max(-col[u], 0), 8), e_hi = min(max(n - col[u], 0), 8);
-                m &= e_hi > e_lo ? ((1u << (e_hi - e_lo)) - 1u) << e_lo : 0u;
-            }
-            if (m) {
-                tlo = min(tlo, col[u] + (int)__builtin_ctz(m));
-                thi = max(thi, col[u] + 31 - (int)__builtin_clz(m));
-            }
-        }
-    }
+    };
+    if (rows == 1) scan(std::true_type{});
+    else scan(std::false_type{});
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         tlo = min(tlo, __shfl_xor(tlo, off, 64));
