@@ -154,7 +154,7 @@ struct AppendArgs {
 // quadrant q mod 4 swaps and negates them. Straight-line code: the library's
 // sincosf carries a large-argument path whose code, repeated for every pair a
 // lane rotates, cost more than the arithmetic.
-__device__ __forceinline__ float2 rope_cs_of_angle(float th) {
+__host__ __device__ __forceinline__ float2 rope_cs_of_angle(float th) {
     const double td = (double)th;
     const double qd = __builtin_rint(td * 0.63661977236758134);   // 2 / pi
     const float r = (float)__builtin_fma(-qd, 1.5707963267948966, td);
@@ -180,7 +180,7 @@ __device__ __forceinline__ float2 rope_cs_of_angle(float th) {
     return float2{(q == 1 || q == 2) ? -cq : cq, (q & 2) ? -sq : sq};
 }
 // cos / sin of pair j's angle at position p: the running product to pair j
-__device__ __forceinline__ float2 rope_cs(int p, int j, float ts) {
+__host__ __device__ __forceinline__ float2 rope_cs(int p, int j, float ts) {
     float th = (float)p;
     for (int i = 0; i < j; ++i) th *= ts;
     return rope_cs_of_angle(th);
