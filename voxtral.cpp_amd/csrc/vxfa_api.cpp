@@ -236,19 +236,21 @@ vxfa::AppendArgs append_args(const vxfa_tensor* k, const vxfa_tensor* v, const v
 }
 
 // Workgroups per (batch, kv head) for the decode split kernel: 2048
-// wavefronts in all (8 per CU), at least 128 live positions per workgroup
-// (one 32-position tile for each of its four wavefronts, and no wavefront
-// with a second tile), and at most kDecodeMaxSplit so the merge stays short.
+// wavefronts in all (8 per CU), at least four tiles of live positions per
+// workgroup (one 16 KB tile for each of its four wavefronts, and no
+// wavefront with a second: 128 positions of an f16 cache, 64 of an F32 one),
+// and at most kDecodeMaxSplit so the merge stays short.
 // Measured in graph replays at 8 kv heads (split + combine, us per layer):
 // n_kv 1024 8.30 with 8 splits against 8.39 with 16; 2048 8.67 (16) against
 // 8.77 (32); 3000 8.83 (24) against 11.12 (48); 4096 9.25 (32) against
 // 11.30 (64); 8192 12.25 (64) against 12.99 (32). With a mask tensor every
 // split workgroup scans the whole mask row, so the caller caps the count
 // (measured on a 2048 window of a 16K cache).
-int choose_split(int64_t pairs, int64_t nkv) {
+int choose_split(int64_t pairs, int64_t nkv, bool kv_f32) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
-    const int64_t by_len = (nkv + 127) / 128;
+    const int64_t per = kv_f32 ? 64 : 128;
+    const int64_t by_len = (nkv + per - 1) / per;
     if (s > by_len) s = by_len;
     if (s > vxfa::kDecodeMaxSplit) s = vxfa::kDecodeMaxSplit;
     if (s < 1) s = 1;
@@ -467,7 +469,7 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             a.kv_hi = (int32_t)hi;
             a.im_causal = 0;   // the range is all the decode kernel needs
         }
-        int S = choose_split(B * Hkv, a.kv_hi - a.kv_lo);
+        int S = choose_split(B * Hkv, a.kv_hi - a.kv_lo, a.kv_f32 != 0);
         if (mask && B > 1) {
             // streams of ragged lengths (a mask row each): the longest sets the
             // time, so split every stream finer, about 2048 workgroups in all
