@@ -249,7 +249,7 @@ vxfa::AppendArgs append_args(const vxfa_tensor* k, const vxfa_tensor* v, const v
 int choose_split(int64_t pairs, int64_t nkv, bool kv_f32) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
-    const int64_t per = kv_f32 ? 64 : 128;
+    const int64_t per = (int64_t)vxfa::kDecodeWaves * (kv_f32 ? 16 : 32);   // one tile per wavefront
     const int64_t by_len = (nkv + per - 1) / per;
     if (s > by_len) s = by_len;
     if (s > vxfa::kDecodeMaxSplit) s = vxfa::kDecodeMaxSplit;
