@@ -66,18 +66,19 @@ constexpr int DEC_THREADS = 64 * DEC_WAVES;
 // (query head, 32 output dims):
 //   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
 // Lane (f, grp) loads float4 f of the slice from splits grp, grp + 8, ...
-// while lane s loads split s's (m, l); all loads issue back to back (loads
-// past the last split read the last record again; their weights are zero), so
-// the merge costs one memory round trip. Wavefront reductions form the
-// weights and the sums, in a fixed order: the output is deterministic.
-template <int D, int G>
+// (MAXS of them, at least n_split / 8) while lane s loads split s's (m, l);
+// all loads issue back to back (loads past the last split read the last
+// record again; their weights are zero), so the merge costs one memory round
+// trip. Wavefront reductions form the weights and the sums, in a fixed order:
+// the output is deterministic (and the same for every MAXS that covers
+// n_split: the extra terms are zeros added at the end of each lane's sum).
+template <int D, int G, int MAXS>
 __global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
     constexpr int CSUB = D / 32;                  // 32-dim slices per head
     constexpr int CF4 = 8;                        // float4 per slice
     constexpr int NGRP = 64 / CF4;                // split groups
-    constexpr int MAXS = kDecodeMaxSplit / NGRP;  // splits per lane
     constexpr int RS = dec_record_floats(D, G);
-    static_assert(kDecodeMaxSplit == 64, "one (m, l) pair per lane");
+    static_assert(kDecodeMaxSplit == 64 && MAXS * NGRP <= kDecodeMaxSplit, "one (m, l) pair per lane");
     const int lane = threadIdx.x;
     const int hq = blockIdx.x / CSUB, sl = blockIdx.x % CSUB;
     const int g = hq / G, h = hq % G;
@@ -652,8 +653,12 @@ static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
         if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32, false>), grid, block, 0, st, a, dv);
         else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32, false>), grid, block, 0, st, a, dv);
     }
-    if (a.n_split > 1)
-        hipLaunchKernelGGL((fa_decode_combine<D, G>), dim3(a.hkv * G * (D / 32), a.b), dim3(64), 0, st, a);
+    // the combine loads ceil(n_split / 8) partial slices per lane
+    const dim3 cgrid(a.hkv * G * (D / 32), a.b);
+    if (a.n_split > 32) hipLaunchKernelGGL((fa_decode_combine<D, G, 8>), cgrid, dim3(64), 0, st, a);
+    else if (a.n_split > 16) hipLaunchKernelGGL((fa_decode_combine<D, G, 4>), cgrid, dim3(64), 0, st, a);
+    else if (a.n_split > 8) hipLaunchKernelGGL((fa_decode_combine<D, G, 2>), cgrid, dim3(64), 0, st, a);
+    else if (a.n_split > 1) hipLaunchKernelGGL((fa_decode_combine<D, G, 1>), cgrid, dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
