@@ -65,20 +65,22 @@ constexpr int DEC_THREADS = 64 * DEC_WAVES;
 // Log-sum-exp merge of the n_split partial records, one wavefront per
 // (query head, 32 output dims):
 //   M = max_s m_s,  w_s = 2^(m_s - M),  O = sum_s w_s O_s / sum_s w_s l_s.
-// Lane (f, grp) loads float4 f of the slice from splits grp, grp + 8, ...
-// (MAXS of them, at least n_split / 8) while lane s loads split s's (m, l);
-// all loads issue back to back (loads past the last split read the last
-// record again; their weights are zero), so the merge costs one memory round
-// trip. Wavefront reductions form the weights and the sums, in a fixed order:
-// the output is deterministic (and the same for every MAXS that covers
-// n_split: the extra terms are zeros added at the end of each lane's sum).
+// Lane (f, grp) = (lane % 8, lane / 8) takes splits grp, grp + 8, ... (MAXS
+// of them, at least n_split / 8): float4 f of each one's slice and its
+// (m, l). All loads issue back to back (loads past the last split read the
+// last record again; their weights are zero), so the merge costs one memory
+// round trip. The lane forms its splits' max, weights and sums itself; the
+// eight split groups then combine over lanes l ^ 8, l ^ 16, l ^ 32 (a DPP
+// row rotation and two lane-swap instructions, on the VALU: the former
+// 64-lane LDS shuffles made three dependent chains of up to six round
+// trips). Fixed order: the output is deterministic.
 template <int D, int G, int MAXS>
 __global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
     constexpr int CSUB = D / 32;                  // 32-dim slices per head
     constexpr int CF4 = 8;                        // float4 per slice
     constexpr int NGRP = 64 / CF4;                // split groups
     constexpr int RS = dec_record_floats(D, G);
-    static_assert(kDecodeMaxSplit == 64 && MAXS * NGRP <= kDecodeMaxSplit, "one (m, l) pair per lane");
+    static_assert(MAXS * NGRP <= kDecodeMaxSplit, "splits per lane");
     const int lane = threadIdx.x;
     const int hq = blockIdx.x / CSUB, sl = blockIdx.x % CSUB;
     const int g = hq / G, h = hq % G;
@@ -88,39 +90,53 @@ __global__ __launch_bounds__(64) void fa_decode_combine(AttnArgs a) {
     const int f = lane % CF4, grp = lane / CF4;
 
     floatx4 o[MAXS];
+    float mi[MAXS], li[MAXS];
 #pragma unroll
     for (int i = 0; i < MAXS; ++i) {
-        const int sp = min(grp + i * NGRP, ns - 1);
-        o[i] = *(const floatx4*)(base + (int64_t)sp * RS + h * D + 32 * sl + 4 * f);
+        const float* rec = base + (int64_t)min(grp + i * NGRP, ns - 1) * RS;
+        o[i] = *(const floatx4*)(rec + h * D + 32 * sl + 4 * f);
+        mi[i] = rec[G * D + h];
+        li[i] = rec[G * D + G + h];
     }
-    const float* r = base + (int64_t)min(lane, ns - 1) * RS + G * D;
-    float m = r[h], l = r[G + h];
-    m = lane < ns ? m : -INFINITY;
-    l = lane < ns ? l : 0.f;
-    float M = m;
+    // over the lanes l ^ 8, l ^ 16, l ^ 32 (the other split groups)
+    auto grp_max = [](float x) {
+        x = fmaxf(x, row_ror<8>(x));
+        const int xi = __builtin_bit_cast(int, x);
+        const auto r = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+        x = fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+        return pair32_max(x);
+    };
+    auto grp_sum = [](float x) {
+        x += row_ror<8>(x);
+        const int xi = __builtin_bit_cast(int, x);
+        const auto r = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+        x = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+        return pair32_sum(x);
+    };
+    float M = -INFINITY;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+    for (int i = 0; i < MAXS; ++i) {
+        const bool live = grp + i * NGRP < ns;
+        mi[i] = live ? mi[i] : -INFINITY;
+        li[i] = live ? li[i] : 0.f;
+        M = fmaxf(M, mi[i]);
+    }
+    M = grp_max(M);
     const float Ms = (M == -INFINITY) ? 0.f : M;
-    const float w = exp2_fast(m - Ms);            // 0 for an empty split (m = -inf)
-    float L = w * l;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
-
+    float L = 0.f;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < MAXS; ++i) {
-        const int sp = grp + i * NGRP;
-        const float ws = __shfl(w, sp & 63, 64);
-        const float wt = sp < ns ? ws : 0.f;
-        acc[0] = fmaf(wt, o[i][0], acc[0]);
-        acc[1] = fmaf(wt, o[i][1], acc[1]);
-        acc[2] = fmaf(wt, o[i][2], acc[2]);
-        acc[3] = fmaf(wt, o[i][3], acc[3]);
+        const float w = exp2_fast(mi[i] - Ms);   // 0 for an empty or absent split (m = -inf)
+        L = fmaf(w, li[i], L);
+        acc[0] = fmaf(w, o[i][0], acc[0]);
+        acc[1] = fmaf(w, o[i][1], acc[1]);
+        acc[2] = fmaf(w, o[i][2], acc[2]);
+        acc[3] = fmaf(w, o[i][3], acc[3]);
     }
+    L = grp_sum(L);
 #pragma unroll
-    for (int off = CF4; off < 64; off <<= 1)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] += shfl_xor(acc[c], off);
+    for (int c = 0; c < 4; ++c) acc[c] = grp_sum(acc[c]);
     if (grp == 0) {
         const float inv = (L == 0.f) ? 0.f : 1.0f / L;
         const floatx4 out = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
