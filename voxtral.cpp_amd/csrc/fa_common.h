@@ -342,10 +342,26 @@ __device__ __forceinline__ void mask_live_range(const uint16_t* base, int64_t ro
     };
     if (rows == 1) scan(std::true_type{});
     else scan(std::false_type{});
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        tlo = min(tlo, __shfl_xor(tlo, off, 64));
-        thi = max(thi, __shfl_xor(thi, off, 64));
+    // wavefront min / max: DPP row rotations, then the lane pairs 16 and 32
+    // apart (VALU lane swaps; no LDS round trips on the way to the range)
+    auto rot_min_max = [&](auto ctl) {   // DPP row_ror by ctl - 0x120
+        constexpr int C = decltype(ctl)::value;
+        tlo = min(tlo, __builtin_amdgcn_update_dpp(0, tlo, C, 0xF, 0xF, false));
+        thi = max(thi, __builtin_amdgcn_update_dpp(0, thi, C, 0xF, 0xF, false));
+    };
+    rot_min_max(std::integral_constant<int, 0x128>{});
+    rot_min_max(std::integral_constant<int, 0x124>{});
+    rot_min_max(std::integral_constant<int, 0x122>{});
+    rot_min_max(std::integral_constant<int, 0x121>{});
+    {
+        const auto l16 = __builtin_amdgcn_permlane16_swap(tlo, tlo, false, false);
+        const auto h16 = __builtin_amdgcn_permlane16_swap(thi, thi, false, false);
+        tlo = min((int)l16[0], (int)l16[1]);
+        thi = max((int)h16[0], (int)h16[1]);
+        const auto l32 = __builtin_amdgcn_permlane32_swap(tlo, tlo, false, false);
+        const auto h32 = __builtin_amdgcn_permlane32_swap(thi, thi, false, false);
+        tlo = min((int)l32[0], (int)l32[1]);
+        thi = max((int)h32[0], (int)h32[1]);
     }
     const int wave = tid >> 6;
     if ((tid & 63) == 0) { red[2 * wave] = tlo; red[2 * wave + 1] = thi; }
