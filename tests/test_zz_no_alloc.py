@@ -65,3 +65,55 @@ def test_noalloc_rejects_staging_beyond_the_scratch(runner):
     assert rc == vx.NO_WORKSPACE
     msg = vx.load().vxfa_last_error(None).decode()
     assert "staging" in msg, msg
+
+
+def test_noalloc_graph_capture_replays(runner):
+    """No-alloc calls captured into a HIP graph, after eager no-alloc calls on
+    the device (the first call on a device looks up the scratch and checks
+    the XCD mapping, which synchronises, so it is made outside capture):
+    decode n_kv 8192 (split records and arrival counters in the scratch) and
+    an F32 K/V prefill (f16 staging in the scratch). Three replays, each
+    followed by eager no-alloc calls of other shapes, match the eager bits."""
+    import torch
+    import gpu_util
+    vx = gpu_util.vxfa
+    cs = [cases.decode_case(8192, seed=311), cases.prefill_case(300, seed=312, kv_f32=True)]
+    devs = [gpu_util.to_device(c) for c in cs]
+    eager = []
+    for c, d in zip(cs, devs):
+        rc, ref = runner.run_noalloc(c, dev=d)
+        assert rc == 0
+        eager.append(ref)
+    outs = []
+    for c in cs:
+        B, Nq, Hq, D = c.out_shape
+        outs.append(torch.zeros(B * Nq * Hq * D, device="cuda", dtype=torch.float32))
+    descs = [gpu_util.descs(c, d) for c, d in zip(cs, devs)]
+    stream = torch.cuda.Stream()
+
+    def step():
+        for c, dd, o in zip(cs, descs, outs):
+            ne, nb = c.dst_ne_nb()
+            dst = vx.desc(o.data_ptr(), vx.F32, ne, nb)
+            rc = vx.flash_attn_ext_noalloc(dd["q"], dd["k"], dd["v"], dd.get("mask"), dst, c.scale,
+                                           stream=stream.cuda_stream)
+            assert rc == 0
+
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    others = [cases.decode_case(1000, seed=313), cases.batched_case(16, capacity=2048, lo=100, hi=2048, seed=314),
+              cases.encoder_case(400, 20, 64, seed=315, kv_f32=True)]
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        for o, ref, c in zip(outs, eager, cs):
+            got = o.cpu().numpy().reshape(c.out_shape)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (rep, c.name)
+        rc, _ = runner.run_noalloc(others[rep])
+        assert rc == 0

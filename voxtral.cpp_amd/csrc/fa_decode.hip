@@ -38,9 +38,17 @@
 //         holds the G query heads replicated 16/G times, so every lane gets
 //         the scores of all G heads for one position: no cross-lane dot
 //         reduction.
-//   K     loaded from HBM straight into the MFMA B-operand layout
-//         (16 positions x 64 contiguous bytes per 128-bit load instruction,
-//         128 bytes as two loads for F32).
+//   K     read like V, D / 8 lanes per row and 16 contiguous bytes per
+//         lane, so one load instruction reads whole 256-byte head rows, then
+//         turned through a wavefront-private LDS tile (rows in, 16-byte chunks
+//         XOR-swizzled by row so the operand reads hit 16 bank groups) into
+//         the MFMA B-operand layout. Against K read straight in that layout
+//         (16 positions x 64 contiguous bytes per load instruction), A/B on
+//         one box, us per layer: n_kv 1024 7.47 -> 7.11, 8192 11.37 -> 10.94,
+//         rope + append 14.05 -> 12.7, F32 cache 20.1 -> 19.3, sliding window
+//         with an implicit mask 7.97 -> 7.42, 32 ragged streams 135 -> 133.5
+//         (a streaming probe of the two patterns alone: 8.0 -> 7.1 us at
+//         n_kv 8192).
 //   V     16 (hd128) or 8 (hd64) lanes per row, fully coalesced 128-bit
 //         loads; P.V on the VALU with fp32 accumulators (each lane owns 8
 //         dims of all G heads); P is handed from the MFMA layout to the V
@@ -150,8 +158,10 @@ struct DecodeDivs {
     DivMod hkv, split, bgrp, hm, bm;
 };
 
+// two wavefronts per SIMD (256 registers per lane, arch + accumulation): the
+// masked f16 variant otherwise took 256 + 2 and ran one per SIMD
 template <int D, int G, bool QF16, bool MASK, bool KV32, bool RING>
-__global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs dv) {
+__global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDivs dv) {
     static_assert(D == 64 || D == 128, "head dim");
     static_assert(G == 1 || G == 2 || G == 4, "GQA group");
     constexpr int KS = D / 32;        // MFMA k-steps of 32 dims
@@ -161,6 +171,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     constexpr int RPI = 64 / CH;      // V rows covered by one load instruction
     constexpr int NV = TP / RPI;
     constexpr int ESZ = KV32 ? 4 : 2; // K/V element size
+    constexpr int NCH = D / 8;        // 16-byte chunks of an f16 row
 
     __shared__ floatx4 lds_p[DEC_WAVES][TP];
     __shared__ float lds_acc[DEC_WAVES][G][D];
@@ -169,6 +180,7 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     __shared__ int lds_red[2 * DEC_WAVES];
     __shared__ half8 lds_q[G * D / 8];   // the group's query heads, f16, [G][D]
     __shared__ float2 lds_rope[D / 2];   // cos / sin of each pair's rotary angle (with rope_pos)
+    __shared__ __align__(16) _Float16 lds_kt[DEC_WAVES * TP * D];   // each wavefront's f16 K tile
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -249,38 +261,43 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
         }
     }
 
-    const int kcol = 8 * (lane >> 4);     // dims owned in the K operand
-    const int vrow = lane / CH;           // row offset owned in the V layout
-    const int vcol = (lane % CH) * 8;     // dims owned in the V layout
+    const int vrow = lane / CH;           // row offset owned in the K / V load layout
+    const int vcol = (lane % CH) * 8;     // dims owned in the K / V load layout
 
-    // One tile in registers: K in the MFMA B-operand layout (position
-    // 16 grp + lane % 16, dims 32 ks + kcol .. + 7), V in the P.V layout (row
-    // vrow + RPI i, dims vcol .. vcol + 7), mask entries of the lane's
-    // position for its four accumulator rows.
+    // One tile in registers: K and V in the load layout (entry i = row
+    // vrow + RPI i, dims vcol .. vcol + 7), mask entries of the lane's MFMA
+    // position (16 grp + lane % 16) for its four accumulator rows.
     struct TileH {
-        half8 k[NG][KS];
+        half8 k[NV];
         half8 v[NV];
         uint16_t m[NG][4];
     };
     struct TileF {
-        floatx4 k[NG][KS][2];
+        floatx4 k[NV][2];
         floatx4 v[NV][2];
         uint16_t m[NG][4];
     };
     using Tile = std::conditional_t<KV32, TileF, TileH>;
-    auto kop = [&](const Tile& T, int grp, int ks) -> half8 {
+    // K entry i as f16 (F32 rounded, as ggml's f16 dot does with Q)
+    auto k8 = [&](const Tile& T, int i) -> half8 {
         if constexpr (KV32) {
             half8 r;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                r[e] = (_Float16)T.k[grp][ks][0][e];
-                r[4 + e] = (_Float16)T.k[grp][ks][1][e];
+                r[e] = (_Float16)T.k[i][0][e];
+                r[4 + e] = (_Float16)T.k[i][1][e];
             }
             return r;
         } else {
-            return T.k[grp][ks];
+            return T.k[i];
         }
     };
+    // The wavefront's f16 K tile in LDS: row r, 16-byte chunk c at chunk
+    // c ^ f(r) of the row (f(r) = r mod 16 at hd 128, (r / 2) mod 8 at hd 64):
+    // the 16 rows one MFMA operand read takes from one column of chunks fall
+    // on 16 different bank groups.
+    _Float16* const kt = lds_kt + wave * TP * D;
+    auto kt_at = [](int r, int c) { return r * D + 8 * (c ^ ((D == 64 ? (r >> 1) : r) & (NCH - 1))); };
     auto vval = [&](const Tile& T, int i, int j) -> float {
         if constexpr (KV32) return T.v[i][j >> 2][j & 3];
         else return (float)T.v[i][j];
@@ -324,22 +341,22 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
             }
             return __umul24((uint32_t)r, nb) + (uint32_t)col;
         };
-        const char* kt = wrap ? kb : kb + (int64_t)rb * a.k_nb1;
+        const char* ktile = wrap ? kb : kb + (int64_t)rb * a.k_nb1;
         const char* vt = wrap ? vb : vb + (int64_t)rb * a.v_nb1;
 #pragma unroll
-        for (int grp = 0; grp < NG; ++grp) {
-            const char* kp = kt + row_off(16 * grp + (lane & 15), knb, kcol * ESZ);
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                if constexpr (KV32) {
-                    T.k[grp][ks][0] = *(const floatx4*)(kp + 128 * ks);
-                    T.k[grp][ks][1] = *(const floatx4*)(kp + 128 * ks + 16);
-                } else if constexpr (masked) {
-                    T.k[grp][ks] = *(const half8*)(kp + 64 * ks);
-                } else {
-                    T.k[grp][ks] = __builtin_nontemporal_load((const half8*)(kp + 64 * ks));
-                }
+        for (int i = 0; i < NV; ++i) {
+            const char* kp = ktile + row_off(vrow + i * RPI, knb, vcol * ESZ);
+            if constexpr (KV32) {
+                T.k[i][0] = *(const floatx4*)(kp);
+                T.k[i][1] = *(const floatx4*)(kp + 16);
+            } else if constexpr (masked) {
+                T.k[i] = *(const half8*)(kp);
+            } else {
+                T.k[i] = __builtin_nontemporal_load((const half8*)(kp));
             }
+        }
+#pragma unroll
+        for (int grp = 0; grp < NG; ++grp) {
             if constexpr (masked) {
                 const uint32_t pos = (uint32_t)(bp + min(16 * grp + (lane & 15), lim));
 #pragma unroll
@@ -430,13 +447,27 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
 
     auto process = [&](const Tile& T, int p0, int pend) {
+        // K rows into the wavefront's LDS tile, MFMA B operands out (position
+        // 16 grp + lane % 16, dims 32 ks + 8 (lane / 16) .. + 7). LDS
+        // instructions of one wavefront execute in order, so its reads see
+        // its writes; the previous tile's reads have returned (its MFMAs used
+        // them) before these writes issue.
+#pragma unroll
+        for (int i = 0; i < NV; ++i) *(half8*)(kt + kt_at(vrow + i * RPI, lane % CH)) = k8(T, i);
+        __builtin_amdgcn_wave_barrier();
+        half8 kop[NG][KS];
+#pragma unroll
+        for (int grp = 0; grp < NG; ++grp)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                kop[grp][ks] = *(const half8*)(kt + kt_at(16 * grp + (lane & 15), 4 * ks + (lane >> 4)));
         floatx4 sc[NG];
 #pragma unroll
         for (int grp = 0; grp < NG; ++grp) {
             sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kop(T, grp, ks), sc[grp], 0, 0, 0);
+                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kop[grp][ks], sc[grp], 0, 0, 0);
         }
         // scores in log2 units; lane holds head (i % G) at position p0 + 16*grp + (lane & 15)
         float x[NG][4];
@@ -494,6 +525,14 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
     };
 
     // ---- main loop: two register sets, the next tile loads during compute ----
+    // (The next tile's loads sit under a branch, so at the join the compiler
+    // counts loads in flight as on the path without them: in a walk of
+    // several tiles each tile's V waits also wait for most of the next tile's
+    // loads. Putting every process() on a straight path (the loop peeled
+    // into three or four copies) removes those waits but raised the kernel
+    // to 256 VGPRs + 48-107 AGPRs, one wavefront per SIMD, or with two forced
+    // per SIMD to 60-420 bytes of scratch per lane: n_kv 8192 11.2 -> 13.1 us
+    // per layer, 32 ragged streams 135 -> 146 us.)
     while (t < t_end) {
         int tn = t + DEC_WAVES;
         if (tn < t_end) load_tile(TB, tn);
@@ -519,12 +558,9 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
             const float* vn = (const float*)((const char*)a.v_new + (int64_t)bkv * a.vn_nb3) + g * D;
             // every load of the row first (one round trip), then rotation (K,
             // with rope_pos; the table holds the row's angles) and rounding
-            floatx4 kr[KS][2], vr[2];
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                kr[ks][0] = *(const floatx4*)(kn + kcol + 32 * ks);
-                kr[ks][1] = *(const floatx4*)(kn + kcol + 32 * ks + 4);
-            }
+            floatx4 kr[2], vr[2];
+            kr[0] = *(const floatx4*)(kn + vcol);
+            kr[1] = *(const floatx4*)(kn + vcol + 4);
             vr[0] = *(const floatx4*)(vn + vcol);
             vr[1] = *(const floatx4*)(vn + vcol + 4);
             auto cvt8 = [&](const floatx4 (&r)[2], int d0, bool rot) {
@@ -536,15 +572,13 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
                 return y;
             };
             const bool rot = a.rope_pos != nullptr;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const half8 kx = cvt8(kr[ks], kcol + 32 * ks, rot);
-#pragma unroll
-                for (int grp = 0; grp < NG; ++grp) TA.k[grp][ks] = kx;
-            }
+            const half8 kx = cvt8(kr, vcol, rot);
             const half8 vx = cvt8(vr, vcol, false);
 #pragma unroll
-            for (int i = 0; i < NV; ++i) TA.v[i] = vx;
+            for (int i = 0; i < NV; ++i) {
+                TA.k[i] = kx;
+                TA.v[i] = vx;
+            }
             if constexpr (masked) {
 #pragma unroll
                 for (int grp = 0; grp < NG; ++grp)
@@ -552,12 +586,10 @@ __global__ __launch_bounds__(DEC_THREADS) void fa_decode(AttnArgs a, DecodeDivs 
                     for (int i = 0; i < 4; ++i) TA.m[grp][i] = mplane[i][pn];
             }
             if (new_live) process(TA, pn, pn + 1);
-            if ((lane & 15) == 0) {
-                _Float16* kc = (_Float16*)(kb + (int64_t)row_of(pn) * a.k_nb1) + kcol;
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) *(half8*)(kc + 32 * ks) = TA.k[0][ks];
+            if (lane < CH) {
+                *(half8*)((_Float16*)(kb + (int64_t)row_of(pn) * a.k_nb1) + vcol) = kx;
+                *(half8*)((_Float16*)(vb + (int64_t)row_of(pn) * a.v_nb1) + vcol) = vx;
             }
-            if (lane < CH) *(half8*)((_Float16*)(vb + (int64_t)row_of(pn) * a.v_nb1) + vcol) = vx;
         }
     }
 

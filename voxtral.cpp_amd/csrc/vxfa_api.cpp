@@ -27,8 +27,8 @@ constexpr size_t kRecordBytes = (size_t)8 << 20;        // e.g. 256 (batch, kv h
 constexpr size_t kStageBytes = (size_t)32 << 20;        // F32 K and V of 8192 rows x 1024 as f16
 
 // Launch-shape overrides for tuning sweeps (VXFA_DECODE_SPLIT,
-// VXFA_PREFILL_WAVES, VXFA_PREFILL_PP), read from the environment;
-// 0 = heuristic.
+// VXFA_PREFILL_WAVES, VXFA_PREFILL_PP, VXFA_PREFILL_PAIR), read from the
+// environment; 0 = heuristic.
 struct Tuning {
     int split_override = 0;
     int waves_override = 0;
@@ -641,9 +641,18 @@ int vxfa_flash_attn_ext_noalloc(const vxfa_tensor* q, const vxfa_tensor* k, cons
     void* ptr = nullptr;
     {
         // first call on this device (the device is current): the array's
-        // device address, once
+        // device address, once. hipGetSymbolAddress may load the code object,
+        // which a stream capture does not allow, so that call must be made
+        // outside capture (later calls may be captured).
         std::lock_guard<std::mutex> lock(g_scratch_mu);
         if (!g_scratch_ptr[device]) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cs) == hipSuccess &&
+                cs != hipStreamCaptureStatusNone) {
+                snprintf(t_noalloc_err, sizeof(t_noalloc_err),
+                         "the first no-alloc call on a device must be made outside stream capture");
+                return VXFA_HIP_ERROR;
+            }
             e = hipGetSymbolAddress(&g_scratch_ptr[device], HIP_SYMBOL(scratch));
             if (e != hipSuccess || !g_scratch_ptr[device]) {
                 g_scratch_ptr[device] = nullptr;
@@ -654,8 +663,12 @@ int vxfa_flash_attn_ext_noalloc(const vxfa_tensor* q, const vxfa_tensor* k, cons
         }
         ptr = g_scratch_ptr[device];
     }
-    Tuning tune;
-    tune.read_env();
+    // the tuning variables, read once per process
+    static const Tuning tune = [] {
+        Tuning t;
+        t.read_env();
+        return t;
+    }();
     // records (decode) and staging (prefill with F32 K/V) are never needed
     // by one call together: both use the whole array
     Workspace w{device, static_cast<float*>(ptr), kScratchBytes, static_cast<_Float16*>(ptr), kScratchBytes,
