@@ -4,13 +4,23 @@
 Headline workload (the `value`): audio-encoder self-attention prefill,
 1500 frames x 20 heads, hd 64, no mask, scale 1/8, 32 layers with distinct
 synthetic N(0,1) tensors. One step = the 32 layer calls. value = algorithmic
-TFLOP/s (4*D*Hq per (q, kv) pair).
+TFLOP/s (4*D*Hq per (q, kv) pair). It is measured after every other
+configuration, so the GPU has left its idle clocks by then (a few ms of
+work after idle ran ~6 % slower than the steady state).
 
 Every configured shape is also measured and reported under "configs":
 decode at n_kv 1024 and 8192, decoder prefill 439 causal, the 100-step
-sliding-window decode and the 32-stream ragged batch. HBM-bound shapes rotate
-over per-layer buffers larger than the 256 MB MALL, so their bytes come from
-HBM; the sliding window is also reported warm (one cache).
+sliding-window decode and the 32-stream ragged batch; besides them the
+shapes the unchanged application passes: the offline encoder with F32 K/V
+(mul_mat outputs), the realtime encoder (1500 frames x 32 heads, hd 64,
+sliding-causal window 750, as a mask tensor and as an implicit mask, f16 and
+F32 K/V) and decoder prefill against the reference's F32 cache. HBM-bound
+shapes rotate over per-layer buffers larger than the 256 MB MALL, so their
+bytes come from HBM; the sliding window is also reported warm (one cache).
+
+--stream-sweep adds a sweep of the read-only streaming probe
+(bench_stream.hip) over grid sizes and loads in flight, at 30 x 32 MiB and
+1 GiB.
 
 The CPU baseline is ggml's one-row algorithm with its AVX2/F16C vector
 kernels (oracle/fa_cpu_simd.c, bit-identical to the scalar oracle in
@@ -85,20 +95,41 @@ def f32s(x):
     return float(np.float32(x))
 
 
-def encoder_layers(torch, n_layers, seq=1500, heads=20, hd=64, seed=1000):
+def encoder_layers(torch, n_layers, seq=1500, heads=20, hd=64, seed=1000, kv_f32=False, mask=None, md=None):
+    """Encoder attention layers: q/k/v [seq][heads][hd] viewed as [hd, seq,
+    heads] (src/voxtral.cpp:1591-1605); K/V f16, or F32 as the unchanged
+    application's mul_mat outputs are; mask: an F16 [seq, seq] tensor (the
+    realtime encoder's window), md: an implicit mask descriptor instead."""
+    kvt, kty, elt = (torch.float32, vxfa.F32, 4) if kv_f32 else (torch.float16, vxfa.F16, 2)
     out = []
     for i in range(n_layers):
         q = randn(torch, (seq, heads, hd), seed + 3 * i).half().float()  # f16-valued F32, as after mul_mat
-        k = randn(torch, (seq, heads, hd), seed + 3 * i + 1, dtype=torch.float16)
-        v = randn(torch, (seq, heads, hd), seed + 3 * i + 2, dtype=torch.float16)
+        k = randn(torch, (seq, heads, hd), seed + 3 * i + 1, dtype=kvt)
+        v = randn(torch, (seq, heads, hd), seed + 3 * i + 2, dtype=kvt)
         dst = torch.empty(seq * heads * hd, device="cuda", dtype=torch.float32)
+        mdesc = vxfa.desc(mask.data_ptr(), vxfa.F16, *views.mask(seq, seq)) if mask is not None else None
         out.append(Layer(vxfa.desc(q.data_ptr(), vxfa.F32, *views.encoder_qkv(seq, heads, hd, 4)),
-                         vxfa.desc(k.data_ptr(), vxfa.F16, *views.encoder_qkv(seq, heads, hd, 2)),
-                         vxfa.desc(v.data_ptr(), vxfa.F16, *views.encoder_qkv(seq, heads, hd, 2)),
-                         None,
+                         vxfa.desc(k.data_ptr(), kty, *views.encoder_qkv(seq, heads, hd, elt)),
+                         vxfa.desc(v.data_ptr(), kty, *views.encoder_qkv(seq, heads, hd, elt)),
+                         mdesc,
                          vxfa.desc(dst.data_ptr(), vxfa.F32, *views.dst(hd, heads, seq)),
-                         f32s(1.0 / math.sqrt(hd)), (q, k, v, dst)))
+                         f32s(1.0 / math.sqrt(hd)), (q, k, v, dst, mask), md))
     return out
+
+
+def window_mask(torch, n, window):
+    """voxtral's realtime-encoder mask (src/voxtral.cpp:2179-2190, cast to
+    F16 at :1564): row q attends kv iff q - window < kv <= q"""
+    i_q = torch.arange(n, device="cuda")[:, None]
+    i_k = torch.arange(n, device="cuda")[None, :]
+    allow = (i_k <= i_q) & (i_k >= i_q - (window - 1))
+    return torch.where(allow, 0.0, float("-inf")).to(torch.float16).contiguous()
+
+
+def window_pairs(n, window):
+    """(q, kv) pairs a sliding-causal window leaves: sum over rows of min(q + 1, window)"""
+    w = min(n, window)
+    return w * (w + 1) // 2 + (n - w) * window
 
 
 def decode_layers(torch, n_layers, n_kv, hq=32, hkv=8, hd=128, capacity=None, seed=2000, batch=1,
@@ -129,20 +160,21 @@ def decode_layers(torch, n_layers, n_kv, hq=32, hkv=8, hd=128, capacity=None, se
     return out
 
 
-def prefill_layers(torch, n_layers, n=439, hq=32, hkv=8, hd=128, seed=3000):
+def prefill_layers(torch, n_layers, n=439, hq=32, hkv=8, hd=128, seed=3000, kv_f32=False):
     i_q = torch.arange(n, device="cuda")[:, None]
     i_k = torch.arange(n, device="cuda")[None, :]
     mask = torch.where(i_k <= i_q, 0.0, float("-inf")).to(torch.float16).contiguous()
+    kvt, kty, elt = (torch.float32, vxfa.F32, 4) if kv_f32 else (torch.float16, vxfa.F16, 2)
     out = []
     for i in range(n_layers):
         q = randn(torch, (n, hq, hd), seed + 3 * i)
-        k = randn(torch, (n, hkv, hd), seed + 3 * i + 1, dtype=torch.float16)
-        v = randn(torch, (n, hkv, hd), seed + 3 * i + 2, dtype=torch.float16)
+        k = randn(torch, (n, hkv, hd), seed + 3 * i + 1, dtype=kvt)
+        v = randn(torch, (n, hkv, hd), seed + 3 * i + 2, dtype=kvt)
         dst = torch.empty(n * hq * hd, device="cuda", dtype=torch.float32)
-        kne, knb = views.kv_cache(n, hkv, hd, n)
+        kne, knb = views.kv_cache(n, hkv, hd, n, elt=elt)
         out.append(Layer(vxfa.desc(q.data_ptr(), vxfa.F32, *views.decoder_q(n, hq, hd)),
-                         vxfa.desc(k.data_ptr(), vxfa.F16, kne, knb),
-                         vxfa.desc(v.data_ptr(), vxfa.F16, kne, knb),
+                         vxfa.desc(k.data_ptr(), kty, kne, knb),
+                         vxfa.desc(v.data_ptr(), kty, kne, knb),
                          vxfa.desc(mask.data_ptr(), vxfa.F16, *views.mask(n, n)),
                          vxfa.desc(dst.data_ptr(), vxfa.F32, *views.dst(hd, hq, n)),
                          f32s(1.0 / math.sqrt(hd)), (q, k, v, dst, mask)))
@@ -233,12 +265,17 @@ def _cpu_inputs(kind, seed):
     f16 = lambda shape, sigma=1.0: (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(
         np.float16).view(np.uint16)
     V = oracle.View
-    if kind == "encoder":
-        seq, heads, hd = 1500, 20, 64
+    if kind in ("encoder", "realtime"):
+        seq, heads, hd = 1500, (20 if kind == "encoder" else 32), 64
         q = rng.standard_normal((seq, heads, hd), dtype=np.float32).astype(np.float16).astype(np.float32)
+        m = None
+        if kind == "realtime":   # sliding-causal window 750 (src/voxtral.cpp:2179-2190)
+            iq, ik = np.arange(seq)[:, None], np.arange(seq)[None, :]
+            allow = (ik <= iq) & (ik >= iq - 749)
+            m = V(np.where(allow, 0, 0xFC00).astype(np.uint16), oracle.F16, *views.mask(seq, seq))
         return (V(q, oracle.F32, *views.encoder_qkv(seq, heads, hd, 4)),
                 V(f16((seq, heads, hd)), oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)),
-                V(f16((seq, heads, hd)), oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)), None, 0.125)
+                V(f16((seq, heads, hd)), oracle.F16, *views.encoder_qkv(seq, heads, hd, 2)), m, 0.125)
     scale = f32s(1 / math.sqrt(128))
     if kind in ("decode1024", "decode8192"):
         n_kv = 1024 if kind == "decode1024" else 8192
@@ -286,14 +323,16 @@ def _cpu_inputs(kind, seed):
     raise ValueError(kind)
 
 
-# configuration -> (input kind, calls timed per repetition, repetitions)
+# configuration -> (input kind, calls timed per repetition, repetitions);
+# about 10 s of CPU work in all at 16 threads
 CPU_SAMPLES = {
-    "encoder_prefill_1500x20_hd64": ("encoder", 1, 9),
-    "decode_nkv1024": ("decode1024", 20, 9),
-    "decode_nkv8192": ("decode8192", 5, 9),
-    "decoder_prefill_439_causal": ("prefill439", 1, 9),
-    "sliding_window_decode_16k_w2048": ("sliding", 5, 9),
-    "batched_ragged_32_streams": ("batched", 1, 9),
+    "encoder_prefill_1500x20_hd64": ("encoder", 1, 41),
+    "realtime_encoder_1500x32_hd64_w750": ("realtime", 1, 21),
+    "decode_nkv1024": ("decode1024", 50, 41),
+    "decode_nkv8192": ("decode8192", 5, 61),
+    "decoder_prefill_439_causal": ("prefill439", 1, 61),
+    "sliding_window_decode_16k_w2048": ("sliding", 20, 41),
+    "batched_ragged_32_streams": ("batched", 1, 41),
 }
 
 
@@ -375,6 +414,60 @@ def stream_read_ceiling(torch, steps, warmup):
                       "one launch per buffer"}
 
 
+def stream_sweep(torch):
+    """Read-only streaming probe (bench_stream.hip) over grid sizes and loads
+    in flight per thread: 30 distinct 32 MiB buffers (one launch each, a
+    decode layer's K/V bytes at n_kv 8192) and one 1 GiB buffer, HIP-graph
+    replays. Rows: (bytes per launch, launches, grid, loads, us per launch,
+    GB/s)."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "bench_stream.so"))
+    lib.bench_stream_sweep.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    big = torch.ones((1 << 30) // 4, device="cuda", dtype=torch.float32)
+    out = torch.zeros(4, device="cuda", dtype=torch.int32)
+    stream = torch.cuda.Stream()
+    rows = []
+
+    def one(nbytes, nbuf, grid, loads, reps=10):
+        def step():
+            for i in range(nbuf):
+                if lib.bench_stream_sweep(big.data_ptr() + i * nbytes, nbytes, grid, loads, out.data_ptr(),
+                                          stream.cuda_stream):
+                    raise RuntimeError("bench_stream_sweep launch failed")
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            step()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                g.replay()
+            start.record(stream)
+            for _ in range(reps):
+                g.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1000.0 / (reps * nbuf)
+        rows.append({"bytes": nbytes, "launches": nbuf, "grid": grid, "loads": loads, "us_per_launch": us,
+                     "gbs": nbytes / (us * 1e-6) / 1e9})
+        log(f"[stream sweep] {nbytes / 2**20:7.0f} MiB x{nbuf:2d} grid {grid:5d} loads {loads:2d}: "
+            f"{us:8.2f} us  {rows[-1]['gbs']:6.0f} GB/s")
+        del g
+
+    for grid in (256, 512, 1024, 2048, 4096):
+        for loads in (4, 8, 16):
+            one(32 << 20, 30, grid, loads)
+    for grid in (1024, 2048, 4096, 8192, 16384):
+        for loads in (8, 16):
+            one(1 << 30, 1, grid, loads)
+    del big
+    torch.cuda.empty_cache()
+    best32 = max((r for r in rows if r["launches"] == 30), key=lambda r: r["gbs"])
+    best1g = max((r for r in rows if r["launches"] == 1), key=lambda r: r["gbs"])
+    return {"rows": rows, "best_32MiB": best32, "best_1GiB": best1g}
+
+
 def load_traffic(kernel_prefix):
     """HBM bytes per launch of the headline kernel, from the committed PMC
     profile (profiles/encoder_prefill_traffic.json): FETCH_SIZE + WRITE_SIZE
@@ -414,6 +507,8 @@ def main():
     ap.add_argument("--only", default="", help="comma list of configs to run (debug)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 256 MiB copy kernel (counter calibration for PMC runs)")
+    ap.add_argument("--stream-sweep", action="store_true",
+                    help="also sweep the read-only streaming probe over grids and loads in flight")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -430,19 +525,6 @@ def main():
     want = lambda name: only is None or name in only
     K, W = args.steps, args.warmup
     configs = {}
-
-    # --- headline: encoder prefill, 32 layers ---
-    enc = encoder_layers(torch, 32)
-    flops_enc = 4.0 * 1500 * 1500 * 64 * 20
-    ms_step, us_layer = time_calls(torch, ctx, enc, K, W)
-    tflops = flops_enc / (us_layer * 1e-6) / 1e12
-    log(f"[encoder] {us_layer:.2f} us/layer  {tflops:.1f} TFLOP/s")
-    configs["encoder_prefill_1500x20_hd64"] = {
-        "us_per_layer": us_layer, "tflops": tflops, "frac_mfma_peak": tflops / MFMA_PEAK_TFLOPS,
-        "flops_per_layer": flops_enc, "layers": 32}
-    headline = (ms_step, us_layer, tflops)
-    del enc
-    torch.cuda.empty_cache()
 
     # --only decode_plain: just the plain decode layers (n_kv 1024 and 8192),
     # for counter runs that must tell those kernels apart
@@ -595,6 +677,72 @@ def main():
         del bl
         torch.cuda.empty_cache()
 
+    if want("prefill"):
+        # the reference's own F32 cache (src/voxtral.cpp:1126-1136): prefill
+        # stages an f16 copy of K and V in the context's workspace first
+        pl = prefill_layers(torch, 30, seed=3100, kv_f32=True)
+        _, us = time_calls(torch, ctx, pl, K, W)
+        fl = 4.0 * 128 * 32 * (439 * 440 // 2)
+        log(f"[decoder prefill 439 causal, F32 cache] {us:.2f} us/layer  {fl / (us * 1e-6) / 1e12:.1f} TFLOP/s")
+        configs["decoder_prefill_439_causal"].update({"f32_cache_us_per_layer": us,
+                                                      "f32_cache_tflops": fl / (us * 1e-6) / 1e12})
+        del pl
+        torch.cuda.empty_cache()
+
+    if want("realtime"):
+        # realtime encoder attention: 1500 frames x 32 heads, hd 64, sliding-
+        # causal window 750 (src/voxtral.cpp:2179-2190, cast at :1564, FA at
+        # :1611), 32 layers; the mask tensor, the implicit mask, and F32 K/V
+        # as the application passes them
+        seq, heads, window = 1500, 32, 750
+        fl = 4.0 * 64 * heads * window_pairs(seq, window)
+        m = window_mask(torch, seq, window)
+        res = {}
+        for tag, kw in (("mask", dict(mask=m)), ("implicit", dict(md=vxfa.mask_desc(vxfa.MASK_CAUSAL, window, 0))),
+                        ("mask_f32_kv", dict(mask=m, kv_f32=True))):
+            rl = encoder_layers(torch, 32, seq, heads, 64, seed=6000, **kw)
+            _, us = time_calls(torch, ctx, rl, K, W)
+            res[tag] = us
+            log(f"[realtime encoder 1500x32 w750, {tag}] {us:.2f} us/layer  {fl / (us * 1e-6) / 1e12:.1f} TFLOP/s")
+            del rl
+            torch.cuda.empty_cache()
+        configs["realtime_encoder_1500x32_hd64_w750"] = {
+            "us_per_layer": res["mask"], "tflops": fl / (res["mask"] * 1e-6) / 1e12,
+            "frac_mfma_peak": fl / (res["mask"] * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, "flops_per_layer": fl,
+            "implicit_mask_us_per_layer": res["implicit"],
+            "implicit_mask_tflops": fl / (res["implicit"] * 1e-6) / 1e12,
+            "f32_kv_us_per_layer": res["mask_f32_kv"], "layers": 32,
+            "note": "q F32 (f16-valued), k/v f16 unless stated; FLOPs count the window's live (q, kv) pairs only"}
+        del m
+
+    if want("encoder_f32"):
+        # the offline encoder as the unchanged application calls it: K/V are
+        # F32 mul_mat outputs (src/voxtral.cpp:1581-1605), staged as f16 first
+        el = encoder_layers(torch, 32, seed=1500, kv_f32=True)
+        _, us = time_calls(torch, ctx, el, K, W)
+        flops_enc = 4.0 * 1500 * 1500 * 64 * 20
+        log(f"[encoder, F32 K/V] {us:.2f} us/layer  {flops_enc / (us * 1e-6) / 1e12:.1f} TFLOP/s")
+        configs["encoder_prefill_1500x20_hd64_f32_kv"] = {"us_per_layer": us,
+                                                           "tflops": flops_enc / (us * 1e-6) / 1e12, "layers": 32}
+        del el
+        torch.cuda.empty_cache()
+
+    if args.stream_sweep:
+        configs["hbm_stream_sweep"] = stream_sweep(torch)
+
+    # --- headline: encoder prefill, 32 layers (after the other configurations: warm GPU) ---
+    enc = encoder_layers(torch, 32)
+    flops_enc = 4.0 * 1500 * 1500 * 64 * 20
+    ms_step, us_layer = time_calls(torch, ctx, enc, K, W)
+    tflops = flops_enc / (us_layer * 1e-6) / 1e12
+    log(f"[encoder] {us_layer:.2f} us/layer  {tflops:.1f} TFLOP/s")
+    configs["encoder_prefill_1500x20_hd64"] = {
+        "us_per_layer": us_layer, "tflops": tflops, "frac_mfma_peak": tflops / MFMA_PEAK_TFLOPS,
+        "flops_per_layer": flops_enc, "layers": 32, "measured": "last of the GPU configurations"}
+    headline = (ms_step, us_layer, tflops)
+    del enc
+    torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         log("[cpu baseline] every configuration on the host cores ...")
@@ -608,10 +756,11 @@ def main():
                 c["speedup_vs_cpu"] = row["us_per_call_default"] / gpu_us
         enc_us = rows["encoder_prefill_1500x20_hd64"]["us_per_call_default"]
         cpu = {"value": flops_enc / (enc_us * 1e-6) / 1e12, "unit": "TFLOP/s", "cores": t_def, "kind": "port",
-               "sample": "every configuration: encoder 1500x20 hd64 (one layer), decode n_kv 1024 and 8192, "
-                         "decoder prefill 439 causal, one sliding-window step (n_kv 16335, window 2048), the "
-                         "32-stream ragged batch; median of 9 repetitions per call through oracle/fa_cpu_simd.c "
-                         "(ggml's one-row algorithm with AVX2/F16C vector kernels, f16 V accumulation), "
+               "sample": "every configuration: encoder 1500x20 hd64 (one layer), realtime encoder 1500x32 hd64 "
+                         "window 750, decode n_kv 1024 and 8192, decoder prefill 439 causal, one sliding-window "
+                         "step (n_kv 16335, window 2048), the 32-stream ragged batch; median of 21-61 repetitions "
+                         "per configuration and thread count through oracle/fa_cpu_simd.c (ggml's one-row "
+                         "algorithm with AVX2/F16C vector kernels, f16 V accumulation), "
                          f"{total:.1f} s of CPU work",
                "threads_default": t_def, "threads_all": t_all,
                "value_all_threads": flops_enc / (rows["encoder_prefill_1500x20_hd64"]["us_per_call_all"] * 1e-6)

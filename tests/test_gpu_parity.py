@@ -234,6 +234,22 @@ def test_encoder_realtime_window(runner):
     check_case(runner, cases.encoder_case(1000, 4, 64, seed=24, window=750))
 
 
+def test_realtime_encoder_full_size(runner):
+    """The realtime encoder's attention at its real shape: 1500 frames x 32
+    heads, hd 64, the 750 sliding-causal window as the F16 mask tensor
+    voxtral fills (3000-byte rows: not 16-byte aligned), as the implicit mask
+    (same bits as the tensor), and with F32 K/V as the application passes them
+    (src/voxtral.cpp:1580-1611, mask :2179-2190, cast :1564)."""
+    from conftest import load_package
+    vx = load_package().vxfa
+    c = cases.encoder_case(1500, 32, 64, seed=25, window=750)
+    out = check_case(runner, c)
+    rc, imp = runner.run_implicit(c, vx.mask_desc(vx.MASK_CAUSAL, 750, 0))
+    assert rc == 0
+    assert np.array_equal(imp.view(np.uint32), out.view(np.uint32))
+    check_case(runner, cases.encoder_case(1500, 32, 64, seed=26, window=750, kv_f32=True))
+
+
 def test_fully_masked_rows_are_zero(runner):
     c = cases.prefill_case(70, hq=4, hkv=2, seed=25)
     m = c.bufs["mask"].reshape(70, 70)
