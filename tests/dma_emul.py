@@ -123,22 +123,49 @@ def pp_copy(sh: Shape, NQT, KVG, NS, kg, wq, bs, blk, mem: Mem):
             mem.issue(blk)
 
 
-def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4, plant=None):
+def pp_block_range(sh: Shape, qg, BM=128, window=None, offset=0):
+    """Blocks [blo, blo + nblk) the workgroup of query tile qg walks: all of
+    them without a mask; under an implicit causal mask (window None: none,
+    0: no lower bound) the blocks holding its rows' live positions
+    i + offset - window < j <= i + offset (the kernel's formula)."""
+    if window is None:
+        return 0, (sh.nkv + 31) // 32
+    qw0 = qg * BM
+    q1 = min(qw0 + BM, sh.nq) - 1
+    lo = qw0 + offset - window + 1 if window > 0 else 0
+    hi = q1 + offset + 1
+    lo, hi = max(lo, 0), min(hi, sh.nkv)
+    if hi <= lo:
+        lo = hi = 0
+    blo = lo // 32
+    return blo, (hi + 31) // 32 - blo
+
+
+def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4, plant=None, window=None, offset=0):
     """The kernel's copy schedule, epoch by epoch (epoch e runs between
     barrier e and barrier e + 1; the prologue's barrier is barrier 0 and
-    iteration t of the main loop runs in epoch t).
+    iteration t of the main loop runs in epoch t), for every workgroup's
+    block range (one range for all without a mask, see pp_block_range).
 
     plant (tests only): "wait_late" waits for one block fewer at the end of
     each iteration, "copy_early" copies block t + NS + 1 in iteration t."""
     BM = 64 * NQT
+    ranges = {pp_block_range(sh, qg, BM, window, offset) for qg in range((sh.nq + BM - 1) // BM)}
+    for blo, nblk in sorted(ranges):
+        _emulate_pp_range(sh, NQT, KVG, NS, plant, blo, nblk)
+    return {"nblk": (sh.nkv + 31) // 32, "ranges": sorted(ranges)}
+
+
+def _emulate_pp_range(sh: Shape, NQT, KVG, NS, plant, blo, nblk):
+    BM = 64 * NQT
     NLD = 4 // NQT
-    nblk = (sh.nkv + 31) // 32
     ni = (nblk + KVG - 1) // KVG
     ahead = NS + 1 if plant == "copy_early" else NS
     slack = 1 if plant == "wait_late" else 0
+    _check(blo >= 0 and (blo + nblk) * 32 < sh.nkv + 32, "block range past n_kv")
     for kg in range(KVG):
-        bs = min(kg * ni, nblk)
-        ng = min(ni, nblk - bs)
+        bs = blo + min(kg * ni, nblk)
+        ng = min(ni, blo + nblk - bs)
         part = ng > 0 and (bs + ng) * 32 > sh.nkv
         nf = ng - (1 if part else 0)
         mems = [Mem() for _ in range(NQT)]
@@ -209,4 +236,3 @@ def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4, plant=None):
             if nxt in copy_epoch:
                 _check(copy_epoch[nxt] > epoch, f"block {blk} overwritten before its read in epoch {epoch}")
         _check(len(copy_epoch) == ng, "not every block of the group was copied")
-    return {"nblk": nblk}

@@ -20,6 +20,30 @@ def test_pp_copies_and_waits_in_bounds(sh):
     emulate_pp(sh)
 
 
+# implicit causal / window masks: every workgroup walks only its rows' live
+# blocks (the realtime encoder's window 750, causal, offsets, windows of one
+# block and less, rows with no live position)
+WINDOWS = [(Shape(1500, 1500, 32, 32), 750, 0), (Shape(1500, 1500, 4, 4), 0, 0), (Shape(439, 439, 4, 4), 0, 0),
+           (Shape(300, 1000, 2, 2), 100, 600), (Shape(200, 200, 2, 2), 1, 0), (Shape(257, 300, 2, 2), 31, 5),
+           (Shape(129, 64, 2, 2), 0, -100), (Shape(100, 4097, 1, 1), 2048, 3997), (Shape(64, 32, 1, 1), 33, 0)]
+
+
+@pytest.mark.parametrize("sh,window,offset", WINDOWS, ids=lambda v: str(v) if not isinstance(v, Shape) else f"nq{v.nq}_nkv{v.nkv}")
+def test_pp_window_copies_and_waits_in_bounds(sh, window, offset):
+    r = emulate_pp(sh, window=window, offset=offset)
+    # the ranges cover exactly the live blocks of each workgroup's rows
+    from dma_emul import pp_block_range
+    for qg in range((sh.nq + 127) // 128):
+        blo, nb = pp_block_range(sh, qg, 128, window, offset)
+        rows = range(qg * 128, min(qg * 128 + 128, sh.nq))
+        live = set()
+        for i in rows:
+            lo = i + offset - window + 1 if window > 0 else 0
+            for j in range(max(lo, 0), min(i + offset + 1, sh.nkv)):
+                live.add(j // 32)
+        assert live == set(range(blo, blo + nb)) or (not live and nb == 0), (qg, blo, nb)
+
+
 @pytest.mark.parametrize("plant", ["wait_late", "copy_early"])
 def test_schedule_emulation_catches_planted_mistakes(plant):
     """A wait one block short, or a copy one block further ahead (into the

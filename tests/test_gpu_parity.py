@@ -242,11 +242,15 @@ def test_realtime_encoder_full_size(runner):
     (src/voxtral.cpp:1580-1611, mask :2179-2190, cast :1564)."""
     from conftest import load_package
     vx = load_package().vxfa
+    import gpu_util
     c = cases.encoder_case(1500, 32, 64, seed=25, window=750)
     out = check_case(runner, c)
     rc, imp = runner.run_implicit(c, vx.mask_desc(vx.MASK_CAUSAL, 750, 0))
     assert rc == 0
-    assert np.array_equal(imp.view(np.uint32), out.view(np.uint32))
+    if HD64_MASK_BITWISE:
+        assert np.array_equal(imp.view(np.uint32), out.view(np.uint32))
+    mx, r, ok = gpu_util.parity(imp, cases.oracle_f64(c), ATOL, RTOL)
+    assert ok, (mx, r)
     check_case(runner, cases.encoder_case(1500, 32, 64, seed=26, window=750, kv_f32=True))
 
 
@@ -397,7 +401,38 @@ def test_implicit_causal_against_filled_cache(runner, n, kv_offset):
 
 def test_implicit_realtime_encoder_window(runner):
     """Realtime encoder: 32 heads, hd 64, causal window 750 (src/voxtral.cpp:2179-2190)."""
-    _implicit(runner, cases.encoder_case(1100, 32, 64, seed=43), offset=0, window=750)
+    _implicit(runner, cases.encoder_case(1100, 32, 64, seed=43), offset=0, window=750, bitwise=HD64_MASK_BITWISE)
+
+
+# hd 64 under an implicit mask runs the pipelined encoder kernel; with a mask
+# tensor it runs the same kernel only when the tensor's rows are live
+# intervals (else the general kernel): bitwise equal once both take it
+HD64_MASK_BITWISE = False
+
+
+@pytest.mark.parametrize("seq,heads,window,offset", [(1500, 4, 750, 0), (1500, 2, 0, 0), (333, 3, 1, 0),
+                                                     (257, 2, 31, 5), (700, 2, 100, 600), (129, 2, 0, -100),
+                                                     (64, 1, 33, 0), (1, 2, 0, 0), (161, 2, 64, 0)])
+def test_implicit_hd64_windows(runner, seq, heads, window, offset):
+    """The pipelined hd 64 kernel under implicit causal / window masks: row
+    ranges that start and end inside a block, windows of one position and of
+    one block less one, offsets past the KV length and before it (rows with
+    no live position give zeros), partial last blocks."""
+    from conftest import load_package
+    import gpu_util
+    vx = load_package().vxfa
+    c = cases.encoder_case(seq, heads, 64, seed=700 + seq + window)
+    m = cases.implicit_mask(seq, seq, offset, window)
+    rc, out = runner.run_implicit(c, vx.mask_desc(vx.MASK_CAUSAL, window, offset))
+    assert rc == 0
+    assert np.isfinite(out).all()
+    cases.with_mask(c, m)
+    for ref in (cases.oracle_ggml(c), cases.oracle_f64(c)):
+        mx, r, ok = gpu_util.parity(out, ref, ATOL, RTOL)
+        _say(f"    implicit hd64 seq={seq} w={window} off={offset}: maxabs={mx:.3e} rel={r:.3e}")
+        assert ok, (mx, r)
+    dead = ~(m != cases.NEG_INF_F16).any(axis=1)
+    assert (out[:, dead] == 0).all()
 
 
 @pytest.mark.parametrize("window", [1, 100, 512])

@@ -1,10 +1,23 @@
-// fa_prefill_pp.hip — encoder self-attention prefill (hd 64, no mask) for
-// gfx950, software-pipelined so the matrix pipe and the VALU overlap inside
-// each wavefront.
+// fa_prefill_pp.hip — encoder self-attention prefill (hd 64) for gfx950,
+// software-pipelined so the matrix pipe and the VALU overlap inside each
+// wavefront.
 //
-// Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the offline
-// encoder call of voxtral.cpp: hd 64, 20 heads, 1500 frames, bidirectional,
-// mask = null, scale = 1/sqrt(64) (src/voxtral.cpp:1580-1613, FA at :1611).
+// Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the encoder
+// calls of voxtral.cpp (src/voxtral.cpp:1580-1613, FA at :1611): the offline
+// encoder (hd 64, 20 heads, 1500 frames, bidirectional, mask = null, scale
+// 1/sqrt(64)) and, with MM = 2, the same op under an implicit causal /
+// window mask: the realtime encoder's sliding-causal window of 750
+// (src/voxtral.cpp:2179-2190; 32 heads).
+//
+// Masks (MM = 2): query row i attends kv j iff i + off - W < j <= i + off
+// (W = 0: no lower bound). A workgroup's KV groups split only the blocks
+// live for some of its 128 rows (at 1500 frames and W = 750 about 28 of the
+// 47 blocks), so dead blocks are never copied or computed. A block that is
+// not wholly live for all 32 rows of a half gets its dead scores set to
+// -inf, in a uniform branch at the top of the half that consumes its S (the
+// S block was computed half an iteration earlier, so the MFMAs and softmax
+// inside the halves keep their interleaving). A row whose running max is
+// still -inf (no live score yet) takes the exact softmax path.
 //
 // Work decomposition
 //   Workgroup = 2 query tiles of 64 rows x 4 KV groups, one wavefront each
@@ -133,8 +146,9 @@ __device__ __forceinline__ void wait_blocks(int k) {
     }
 }
 
-template <bool QF16, bool C8>
+template <bool QF16, bool C8, int MM>
 __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm, int nblk, int ni) {
+    static_assert(MM == 0 || MM == 2, "no mask, or an implicit causal / window mask");
     using namespace pp;
     static_assert(NLD * NQT == 4, "a block's 4 load instructions per matrix split evenly");
     static_assert(8 * 2 * NLD < 64 && NS <= 8, "vmcnt range of wait_blocks");
@@ -157,9 +171,22 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
 
-    // blocks [bs, bs + ng) of this KV group
-    const int bs = min(kg * ni, nblk);
-    const int ng = min(ni, nblk - bs);
+    // blocks [blo, blo + nblk) hold the live KV positions of the workgroup's
+    // rows (all of them without a mask); KV group kg takes [bs, bs + ng)
+    int blo = 0;
+    if constexpr (MM == 2) {
+        const int64_t q1 = min(qw0 + BM, a.nq) - 1;      // the workgroup's last real row
+        int64_t lo = a.im_window > 0 ? (int64_t)qw0 + a.im_offset - a.im_window + 1 : 0;
+        int64_t hi = q1 + a.im_offset + 1;                // exclusive
+        lo = lo < 0 ? 0 : lo;
+        hi = hi > a.nkv ? a.nkv : hi;
+        if (hi <= lo) lo = hi = 0;
+        blo = (int)(lo / BK);
+        nblk = (int)((hi + BK - 1) / BK) - blo;
+        ni = (nblk + KVG - 1) / KVG;
+    }
+    const int bs = blo + min(kg * ni, nblk);
+    const int ng = min(ni, blo + nblk - bs);
 
     // ---- Q: coalesced loads by the whole workgroup (issued first, so their
     // latency overlaps the first K/V blocks) -----------------------------------
@@ -311,6 +338,37 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         for (int j = 0; j < 16; ++j)
             if (kv0 + pf_kv_of(hh, j) >= a.nkv) sc[j] = -INFINITY;
     };
+    // MM = 2: the live positions [rlo, rhi] of the lane's row in each half
+    // (clamped to [-1, n_kv]), and per half the largest lower bound and the
+    // smallest upper bound over its 32 rows (a block inside both is wholly
+    // live for the half)
+    int rlo[2] = {0, 0}, rhi[2] = {0, 0}, hlo[2] = {0, 0}, hhi[2] = {0, 0};
+    if constexpr (MM == 2) {
+        auto clampkv = [&](int64_t x) { return (int)(x < -1 ? -1 : (x > a.nkv ? a.nkv : x)); };
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int64_t r0 = (int64_t)qw0 + 64 * wq + 32 * x;
+            const int64_t wb = a.im_window > 0 ? a.im_offset - a.im_window + 1 : INT64_MIN / 2;
+            rlo[x] = clampkv(r0 + nl + wb);
+            rhi[x] = clampkv(r0 + nl + a.im_offset);
+            hlo[x] = clampkv(r0 + 31 + wb);
+            hhi[x] = clampkv(r0 + a.im_offset);
+        }
+    }
+    // MM = 2: block blk (of this group) for half x; a uniform branch, taken
+    // only for blocks not wholly live for the half's rows
+    auto mask_fix = [&](floatx16& sc, int blk, int x) {
+        if constexpr (MM == 2) {
+            const int kv0 = (bs + blk) * BK;
+            if (!(kv0 >= hlo[x] && kv0 + BK - 1 <= hhi[x])) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int kv = kv0 + pf_kv_of(hh, j);
+                    sc[j] = (kv < rlo[x] || kv > rhi[x]) ? -INFINITY : sc[j];
+                }
+            }
+        }
+    };
     // P = 2^(c s - m) for the lane's 16 scores, as two f16 B operands, and
     // their sum. With C8 (scale exactly 1/8) c is a literal and x = c s - m
     // compiles to v_fmamk_f32, which issues at twice the rate of the
@@ -394,7 +452,11 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
                 __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
             }
         }
-        if (__any(!(ls <= 256.0f))) {   // 2^TAU; also true for inf / NaN
+        // 2^TAU (also true for inf / NaN); with a mask, also a row that has
+        // no live score yet (its P above were taken against m = 0)
+        bool slow = !(ls <= 256.0f);
+        if constexpr (MM != 0) slow = slow || m == -INFINITY;
+        if (__any(slow)) {
             raise(block_max(sc), m, l, o);
             ls = exps(sc, m, p);
         }
@@ -434,6 +496,8 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         read_v(0, vr);
         s_mfma(sa, qa, kr);
         s_mfma(sb, qb, kr);
+        mask_fix(sa, 0, 0);
+        mask_fix(sb, 0, 1);
         softmax_exact(sa, ma, la, oa, pa);
         // the loop's softmax needs a finite running max to start from
         mb = block_max(sb);
@@ -451,6 +515,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     for (int t = 0; t + 1 < nf; ++t) {
         if (t == 1 && NS < ng) issue(NS);
         read_k(t + 1, kr);
+        if (t > 0) mask_fix(sb, t, 1);   // S_B(t), from H2 of the previous iteration
         // H1: PV_A(t), S_A(t+1) on the matrix pipe; softmax of S_B(t). The
         // MFMAs come first in the source so they share a basic block with
         // the softmax's fast path (its rare rescale branch closes the block)
@@ -461,6 +526,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb);
         if ((t == 0 ? NS - 1 : t + NS) < ng) issue(t == 0 ? NS - 1 : t + NS);
         // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
+        mask_fix(sa, t + 1, 0);
         pv_mfma(ob, pb, vr);
         read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
         s_mfma(sb, qb, kr);
@@ -473,6 +539,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     // (no loads are issued from here on)
     if (nf > 0) {
         // last full block: PV_A, softmax of S_B, PV_B
+        if (nf > 1) mask_fix(sb, nf - 1, 1);
         pv_mfma(oa, pa, vr);
         softmax_exact(sb, mb, lb, ob, pb);
         pv_mfma(ob, pb, vr);
@@ -488,6 +555,8 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         read_v(tp, vr);
         tail_fix(sa, tp);
         tail_fix(sb, tp);
+        mask_fix(sa, tp, 0);
+        mask_fix(sb, tp, 1);
         softmax_exact(sa, ma, la, oa, pa);
         softmax_exact(sb, mb, lb, ob, pb);
         pv_mfma(oa, pa, vr);
@@ -588,7 +657,20 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     }
 }
 
-// hd 64 without a mask: 128 query rows x 4 KV groups per workgroup.
+// hd 64 without a mask or with an implicit causal / window mask: 128 query
+// rows x 4 KV groups per workgroup.
+template <int MM>
+static void launch_pp_mm(const AttnArgs& a, const GridMap& gm, int nblk, int ni, bool is_c8, const dim3& grid,
+                         const dim3& block, hipStream_t st) {
+    if (a.q_f16) {
+        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<true, true, MM>), grid, block, 0, st, a, gm, nblk, ni);
+        else hipLaunchKernelGGL((fa_prefill64_pp<true, false, MM>), grid, block, 0, st, a, gm, nblk, ni);
+    } else {
+        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<false, true, MM>), grid, block, 0, st, a, gm, nblk, ni);
+        else hipLaunchKernelGGL((fa_prefill64_pp<false, false, MM>), grid, block, 0, st, a, gm, nblk, ni);
+    }
+}
+
 hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
     using namespace pp;
     const int nqg = (a.nq + BM - 1) / BM;
@@ -601,13 +683,9 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
     const bool is_c8 = fabsf(a.scale_log2) == c8 && __builtin_bit_cast(uint32_t, c8) == 0x3e38aa3bu;
     const GridMap gm = GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
-    if (a.q_f16) {
-        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<true, true>), grid, block, 0, st, a, gm, nblk, ni);
-        else hipLaunchKernelGGL((fa_prefill64_pp<true, false>), grid, block, 0, st, a, gm, nblk, ni);
-    } else {
-        if (is_c8) hipLaunchKernelGGL((fa_prefill64_pp<false, true>), grid, block, 0, st, a, gm, nblk, ni);
-        else hipLaunchKernelGGL((fa_prefill64_pp<false, false>), grid, block, 0, st, a, gm, nblk, ni);
-    }
+    if (a.mask) return hipErrorInvalidValue;
+    if (a.im_causal) launch_pp_mm<2>(a, gm, nblk, ni, is_c8, grid, block, st);
+    else launch_pp_mm<0>(a, gm, nblk, ni, is_c8, grid, block, st);
     return hipGetLastError();
 }
 

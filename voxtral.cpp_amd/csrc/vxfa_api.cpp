@@ -511,10 +511,11 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             a.k_nb3 = a.v_nb3 = Nkv * Hkv * D * 2;
             a.kv_f32 = 0;
         }
-        if (D == 64 && !mask && !implicit && !rope && scale != 0.0f && w.tune.pp_enabled) {
+        if (D == 64 && !mask && !rope && scale != 0.0f && w.tune.pp_enabled) {
             // (scale 0 goes to the general kernel: the pipelined one folds the
             // scale into the exponent and scores the partial block's dead rows -inf)
-            // encoder prefill: the software-pipelined hd 64 kernel
+            // encoder prefill: the software-pipelined hd 64 kernel, also under
+            // an implicit causal / window mask (the realtime encoder's window)
             e = vxfa::launch_prefill64_pp(a, st);
         } else if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled && vxfa::prefill_pair_fits(a)) {
             // short masked prefill (voxtral's decoder prefill): paired query
