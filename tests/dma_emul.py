@@ -141,16 +141,71 @@ def pp_block_range(sh: Shape, qg, BM=128, window=None, offset=0):
     return blo, (hi + 31) // 32 - blo
 
 
-def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4, plant=None, window=None, offset=0):
+NEG_INF_F16 = 0xFC00
+
+
+def mask_row_interval(row, mis):
+    """The pre-pass of a mask tensor (mask_rows_kernel) for one F16 mask row
+    (uint16 array of n entries) whose first entry sits mis bytes (even, < 16)
+    past a 16-byte boundary: the kernel reads 16-byte chunks c = 0 .. nch - 1
+    from the boundary, entry e of chunk c being column (16 c - mis) / 2 + e,
+    drops the columns outside [0, n), and returns (lo, hi) when the row is
+    +-0 on [lo, hi] and -inf elsewhere, (n, -1) when every entry is -inf,
+    (-2, -2) otherwise."""
+    n = len(row)
+    nch = (mis + 2 * n + 15) // 16
+    lo, hi, nonzero = 1 << 31, -1, False
+    cols = []
+    for c in range(nch):
+        for e in range(8):
+            col = (16 * c - mis) // 2 + e
+            cols.append(col)
+            if col < 0 or col >= n or row[col] == NEG_INF_F16:
+                continue
+            lo, hi = min(lo, col), max(hi, col)
+            nonzero = nonzero or (int(row[col]) & 0x7FFF) != 0
+    _check(sorted(c for c in cols if 0 <= c < n) == list(range(n)), "the chunks miss or repeat a column")
+    _check(all(-8 <= c < n + 8 for c in cols), "a chunk lies wholly outside the row")
+    hole = False
+    if not nonzero and hi >= lo:
+        hole = any(lo < c < hi and row[c] == NEG_INF_F16 for c in cols if 0 <= c < n)
+    if nonzero or hole:
+        return (-2, -2)
+    return (n, -1) if hi < lo else (lo, hi)
+
+
+def pp_block_range_table(sh: Shape, qg, table, BM=128):
+    """Blocks [blo, blo + nblk) the workgroup of query tile qg walks under a
+    mask tensor (the kernel's MM = 1 logic): with any row of class (-2, -2)
+    among its rows, every block; else the blocks between the smallest lo and
+    the largest hi of its rows' intervals (none when all are empty). Rows
+    past n_q count as empty. table: the pre-pass output of the rows of one
+    (plane, batch)."""
+    ivl = [tuple(table[r]) if r < sh.nq else (sh.nkv, -1) for r in range(qg * BM, qg * BM + BM)]
+    if any(v[0] == -2 for v in ivl):
+        return 0, (sh.nkv + 31) // 32
+    live = [v for v in ivl if 0 <= v[0] <= v[1]]
+    if not live:
+        return 0, 0
+    wlo, whi = min(v[0] for v in live), max(v[1] for v in live)
+    blo = wlo // 32
+    return blo, (whi + 32) // 32 - blo
+
+
+def emulate_pp(sh: Shape, NQT=2, KVG=4, NS=4, plant=None, window=None, offset=0, table=None):
     """The kernel's copy schedule, epoch by epoch (epoch e runs between
     barrier e and barrier e + 1; the prologue's barrier is barrier 0 and
     iteration t of the main loop runs in epoch t), for every workgroup's
-    block range (one range for all without a mask, see pp_block_range).
+    block range (one range for all without a mask, see pp_block_range; a
+    mask tensor's pre-pass table: pp_block_range_table).
 
     plant (tests only): "wait_late" waits for one block fewer at the end of
     each iteration, "copy_early" copies block t + NS + 1 in iteration t."""
     BM = 64 * NQT
-    ranges = {pp_block_range(sh, qg, BM, window, offset) for qg in range((sh.nq + BM - 1) // BM)}
+    if table is not None:
+        ranges = {pp_block_range_table(sh, qg, table, BM) for qg in range((sh.nq + BM - 1) // BM)}
+    else:
+        ranges = {pp_block_range(sh, qg, BM, window, offset) for qg in range((sh.nq + BM - 1) // BM)}
     for blo, nblk in sorted(ranges):
         _emulate_pp_range(sh, NQT, KVG, NS, plant, blo, nblk)
     return {"nblk": (sh.nkv + 31) // 32, "ranges": sorted(ranges)}

@@ -4,7 +4,10 @@
 //   gidx = xcd < r8 ? xcd (q8 + 1) : r8 (q8 + 1) + (xcd - r8) q8, + lin / 8
 //   qt = gidx % nqt, h = gidx / nqt % hq, b = gidx / (nqt hq),
 //   hk = h / (hq / hkv), bkv = b / (B / bk)
-// and that the map is a bijection of [0, nwg) onto the (qt, h, b) triples.
+// and that the map is a bijection of [0, nwg) onto the (qt, h, b) triples;
+// and the F32 K/V staging kernel's split of its flat index i (8-element
+// groups of a [b][n][h][d] buffer) into (row, element, kv head, position,
+// batch) by shifts and DivMod, against the plain division.
 #include "../../voxtral.cpp_amd/csrc/fa_common.h"
 #include <cstdio>
 #include <cstdlib>
@@ -66,6 +69,23 @@ int main() {
             if (qt != gidx % nqt || h != (gidx / nqt) % hq || b != gidx / (nqt * hq)) return fail("locate", lin, gidx, nwg);
             if (hk != h / (hq / hkv) || bkv != b / (B / bk)) return fail("locate kv", lin, hk, bkv);
             if (gidx < 0 || gidx >= nwg || seen[gidx]++) return fail("bijection", lin, gidx, nwg);
+            ++checks;
+        }
+    }
+    // staging index (to_f16_kv_kernel): i -> r = i >> log2(d/8), e = 8 (i - r (d/8)),
+    // hh = r % h, pos = (r / h) % n, bb = r / h / n; element 8 i of the buffer
+    const int stg[][4] = {{64, 1500, 20, 1}, {128, 439, 8, 1}, {64, 7, 3, 5}, {128, 8192, 8, 2}, {64, 1, 1, 1}};
+    for (auto& s4 : stg) {
+        const uint32_t d = s4[0], n = s4[1], h = s4[2], b = s4[3];
+        uint32_t l2 = 0;
+        while ((1u << l2) < d / 8) ++l2;
+        const vxfa::DivMod dh = vxfa::DivMod::make(h), dn = vxfa::DivMod::make(n);
+        const uint32_t total8 = b * n * h * (d / 8);
+        for (uint32_t i = 0; i < total8; ++i) {
+            const uint32_t r = i >> l2, e = (i - (r << l2)) * 8;
+            const uint32_t r2 = dh.div(r), hh = r - r2 * dh.d, bb = dn.div(r2), pos = r2 - bb * dn.d;
+            if (bb >= b || pos >= n || hh >= h || e >= d) return fail("stage range", i, d, n);
+            if ((uint64_t)i * 8 != (((uint64_t)bb * n + pos) * h + hh) * d + e) return fail("stage index", i, d, n);
             ++checks;
         }
     }

@@ -22,7 +22,8 @@ hipError_t launch_prefill_pair(const AttnArgs&, hipStream_t) { return hipErrorIn
 bool prefill_pair_fits(const AttnArgs&) { return true; }
 hipError_t launch_zero(float*, int64_t, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_kv_append(const AppendArgs&, hipStream_t) { return hipErrorInvalidValue; }
-hipError_t launch_to_f16(const float*, int64_t, int64_t, int64_t, int, int, int, int, _Float16*, hipStream_t) {
+hipError_t launch_to_f16_kv(const float*, int64_t, int64_t, int64_t, const float*, int64_t, int64_t, int64_t, int, int,
+                            int, int, _Float16*, _Float16*, hipStream_t) {
     return hipErrorInvalidValue;
 }
 }  // namespace vxfa

@@ -404,10 +404,10 @@ def test_implicit_realtime_encoder_window(runner):
     _implicit(runner, cases.encoder_case(1100, 32, 64, seed=43), offset=0, window=750, bitwise=HD64_MASK_BITWISE)
 
 
-# hd 64 under an implicit mask runs the pipelined encoder kernel; with a mask
-# tensor it runs the same kernel only when the tensor's rows are live
-# intervals (else the general kernel): bitwise equal once both take it
-HD64_MASK_BITWISE = False
+# hd 64 under an implicit mask and under a mask tensor runs the pipelined
+# encoder kernel; a tensor whose rows are live intervals (a pre-pass finds
+# them) takes the implicit mask's path with the same bounds: bitwise equal
+HD64_MASK_BITWISE = True
 
 
 @pytest.mark.parametrize("seq,heads,window,offset", [(1500, 4, 750, 0), (1500, 2, 0, 0), (333, 3, 1, 0),
@@ -433,6 +433,69 @@ def test_implicit_hd64_windows(runner, seq, heads, window, offset):
         assert ok, (mx, r)
     dead = ~(m != cases.NEG_INF_F16).any(axis=1)
     assert (out[:, dead] == 0).all()
+    # the same mask as an F16 tensor
+    rc, mt = runner.run(c)
+    assert rc == 0
+    assert np.array_equal(mt.view(np.uint32), out.view(np.uint32))
+
+
+def _mask_planes(c, planes):
+    """Replace c's mask by the [nkv, nq, P, 1] tensor of the P planes (uint16
+    [nq, nkv] each); head h reads plane h % P."""
+    nq, nkv = planes[0].shape
+    m = np.ascontiguousarray(np.stack(planes))
+    c.bufs.pop("mask", None)
+    c.views.pop("mask", None)
+    c.add("mask", "mask", m, oracle.F16, (nkv, nq, len(planes), 1),
+          (2, 2 * nkv, 2 * nkv * nq, 2 * nkv * nq * len(planes)))
+    return c
+
+
+def _hd64_mask(kind, seq, rng):
+    m = cases.implicit_mask(seq, seq, 0, 100)
+    if kind == "holes":           # -inf holes inside the window of rows 130 .. 140
+        for r in range(min(130, seq - 1), min(141, seq)):
+            if r >= 2:
+                m[r, r - 1] = cases.NEG_INF_F16
+    elif kind == "bias":          # finite values on every live entry
+        bias = cases.f16_bits(rng.uniform(-3, 3, size=m.shape).astype(np.float32))
+        m = np.where(m == cases.NEG_INF_F16, m, bias).astype(np.uint16)
+    elif kind == "minus_zero":    # -0 entries are live
+        m = np.where(m == 0, np.uint16(0x8000), m).astype(np.uint16)
+    elif kind == "empty_rows":    # rows with no live entry
+        m[::7] = cases.NEG_INF_F16
+    elif kind == "islands":       # one live run per row, anywhere
+        m[:] = cases.NEG_INF_F16
+        for r in range(seq):
+            lo = int(rng.integers(0, seq))
+            m[r, lo:int(rng.integers(lo, seq)) + 1] = 0
+    return m
+
+
+@pytest.mark.parametrize("kind", ["holes", "bias", "minus_zero", "empty_rows", "islands"])
+@pytest.mark.parametrize("seq", [300, 161])
+def test_hd64_mask_tensor(runner, kind, seq):
+    """hd 64 prefill with a mask tensor on the pipelined kernel: rows that are
+    live intervals (window, islands, -0, empty rows) take the interval path;
+    a workgroup with holes or finite values adds the mask per element. An odd
+    n_kv (161) puts the mask rows off 16-byte alignment."""
+    rng = np.random.default_rng(900 + seq + len(kind))
+    c = cases.encoder_case(seq, 4, 64, seed=900 + seq)
+    cases.with_mask(c, _hd64_mask(kind, seq, rng))
+    out = check_case(runner, c)
+    m = c.bufs["mask"]
+    dead = ~(m != cases.NEG_INF_F16).any(axis=1)
+    assert (out[:, dead] == 0).all()
+
+
+def test_hd64_mask_tensor_planes(runner):
+    """Two mask planes (head h reads plane h % 2): a window on one, finite
+    values on the other, so one plane's workgroups take the interval path
+    and the other's the per-element path."""
+    rng = np.random.default_rng(950)
+    c = cases.encoder_case(400, 4, 64, seed=950)
+    _mask_planes(c, [_hd64_mask("window", 400, rng), _hd64_mask("bias", 400, rng)])
+    check_case(runner, c)
 
 
 @pytest.mark.parametrize("window", [1, 100, 512])

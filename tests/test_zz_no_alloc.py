@@ -55,6 +55,14 @@ def test_noalloc_prefill_and_f32_staging(runner):
     _same(runner, cases.prefill_case(100, seed=307, kv_f32=True))
 
 
+def test_noalloc_mask_tensor_after_staging(runner):
+    """hd 64 prefill with a mask tensor: the pre-pass's row intervals sit in
+    the scratch after the f16 staging of F32 K/V (a context keeps them in its
+    own region): the same bits either way, then a smaller masked call."""
+    _same(runner, cases.encoder_case(600, 20, 64, seed=309, window=300, kv_f32=True), oracle=True)
+    _same(runner, cases.encoder_case(200, 4, 64, seed=310, window=50), oracle=True)
+
+
 def test_noalloc_rejects_staging_beyond_the_scratch(runner):
     """F32 K and V of 16384 rows x 8 x 128 need 64 MiB of f16 staging: beyond
     the 8 MiB scratch, the call returns VXFA_NO_WORKSPACE and launches nothing."""

@@ -63,6 +63,11 @@ struct AttnArgs {
     const float* k_new;
     const float* v_new;
     int64_t kn_nb3, vn_nb3;
+    // hd 64 prefill with a mask tensor: per mask row (batch bm_i, plane p,
+    // row q at (bm_i * hm + p) * nq + q) the live interval {lo, hi} when the
+    // row is 0 on [lo, hi] and -inf elsewhere ({n_kv, -1}: no live entry),
+    // else {-2, -2}; written by a pre-pass launch into workspace scratch
+    int2* mask_rows;
 };
 
 // n / d for 0 <= n < 2^31 by a multiply-high, an add and a shift, with the
@@ -447,6 +452,9 @@ constexpr int kDecodeWaves = 4;      // wavefronts per decode workgroup
 // a multiple of 4 so every record starts 16-byte aligned.
 constexpr int dec_record_floats(int D, int G) { return G * D + ((2 * G + 3) & ~3); }
 hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_t stream);
+// hd 64 prefill on the pipelined kernel: no mask, an implicit mask, or a mask
+// tensor (a.mask_rows: workspace for nq * hm * bm intervals, filled first by
+// a pre-pass launch)
 hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t stream);
 // masked hd 128 prefill with n_kv <= 512 (a mask tensor or an implicit mask;
 // a rotary embedding of F32 Q)
@@ -455,8 +463,9 @@ hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t stream);
 bool prefill_pair_fits(const AttnArgs& a);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
-// F32 -> f16 copy of a [D, n, H, B] view (byte strides nb1..nb3, rows
-// contiguous) into a contiguous [B][n][H][D] f16 buffer.
-hipError_t launch_to_f16(const float* src, int64_t nb1, int64_t nb2, int64_t nb3, int d, int n, int h, int b,
-                         _Float16* dst, hipStream_t stream);
+// F32 -> f16 copies of the K and V views [D, n, H, B] (byte strides nb1..nb3,
+// rows contiguous) into contiguous [B][n][H][D] f16 buffers, one launch
+hipError_t launch_to_f16_kv(const float* k, int64_t k_nb1, int64_t k_nb2, int64_t k_nb3, const float* v,
+                            int64_t v_nb1, int64_t v_nb2, int64_t v_nb3, int d, int n, int h, int b, _Float16* dk,
+                            _Float16* dv, hipStream_t stream);
 }  // namespace vxfa

@@ -751,41 +751,63 @@ hipError_t launch_zero(float* dst, int64_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
-// F32 -> f16 (round to nearest even) copy of the view src [d, n, h, b] into a
-// contiguous [b][n][h][d] buffer: one thread per 8 elements (two 16-byte
-// loads, one 16-byte store). Used to stage F32 K/V for the prefill kernels.
-__global__ __launch_bounds__(256) void to_f16_kernel(const float* src, int64_t nb1, int64_t nb2, int64_t nb3, int d,
-                                                     int n, int h, int64_t total8, _Float16* dst) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total8) return;
-    const int c8 = d / 8;
-    int64_t r = i / c8;
-    const int e = (int)(i - r * c8) * 8;
-    const int hh = (int)(r % h);
-    r /= h;
-    const int pos = (int)(r % n);
-    const int bb = (int)(r / n);
-    const floatx4* p = (const floatx4*)((const char*)src + (int64_t)pos * nb1 + (int64_t)hh * nb2 + (int64_t)bb * nb3) +
-                       e / 4;
-    const floatx4 x0 = p[0], x1 = p[1];
+// F32 -> f16 (round to nearest even) copies of the K and V views [d, n, h, b]
+// into contiguous [b][n][h][d] buffers, both in one launch: blockIdx.y picks
+// K or V, each thread converts 8 consecutive elements (two 16-byte loads, one
+// 16-byte store). The flat index splits by shifts (d / 8 is a power of two)
+// and host-made reciprocals, all 32-bit. Used to stage F32 K/V for the
+// prefill kernels, whose tiles reach LDS by direct global-to-LDS copies.
+struct StageArgs {
+    const float* src[2];
+    int64_t nb1[2], nb2[2], nb3[2];
+    _Float16* dst[2];
+    uint32_t total8;       // 8-element groups per tensor
+    uint32_t c8_log2;      // log2(d / 8)
+    DivMod h, n;
+};
+
+__global__ __launch_bounds__(256) void to_f16_kv_kernel(StageArgs sa) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= sa.total8) return;
+    const int t = blockIdx.y;
+    const uint32_t r = i >> sa.c8_log2;                  // row index (b, pos, h)
+    const uint32_t e = (i - (r << sa.c8_log2)) * 8;      // first element in the row
+    const uint32_t r2 = sa.h.div(r);
+    const uint32_t hh = r - r2 * sa.h.d;
+    const uint32_t bb = sa.n.div(r2);
+    const uint32_t pos = r2 - bb * sa.n.d;
+    const floatx4* p = (const floatx4*)((const char*)sa.src[t] + (int64_t)pos * sa.nb1[t] + (int64_t)hh * sa.nb2[t] +
+                                        (int64_t)bb * sa.nb3[t]) + e / 4;
+    const floatx4 x0 = __builtin_nontemporal_load(p), x1 = __builtin_nontemporal_load(p + 1);
     half8 y;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         y[j] = (_Float16)x0[j];
         y[4 + j] = (_Float16)x1[j];
     }
-    *(half8*)(dst + i * 8) = y;
+    *(half8*)(sa.dst[t] + (int64_t)i * 8) = y;
 }
 
-hipError_t launch_to_f16(const float* src, int64_t nb1, int64_t nb2, int64_t nb3, int d, int n, int h, int b,
-                         _Float16* dst, hipStream_t st) {
-    if (d % 8 || n < 0 || h < 0 || b < 0) return hipErrorInvalidValue;
+hipError_t launch_to_f16_kv(const float* k, int64_t k_nb1, int64_t k_nb2, int64_t k_nb3, const float* v, int64_t v_nb1,
+                            int64_t v_nb2, int64_t v_nb3, int d, int n, int h, int b, _Float16* dk, _Float16* dv,
+                            hipStream_t st) {
+    if (d % 8 || (d / 8 & (d / 8 - 1)) || n < 0 || h < 0 || b < 0) return hipErrorInvalidValue;
     const int64_t total8 = (int64_t)b * n * h * (d / 8);
     if (total8 == 0) return hipSuccess;
-    const int64_t blocks = (total8 + 255) / 256;
-    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, st, src, nb1, nb2, nb3, d, n, h, total8,
-                       dst);
+    if (total8 > 0x7fffff00) return hipErrorInvalidValue;
+    StageArgs sa;
+    sa.src[0] = k; sa.src[1] = v;
+    sa.nb1[0] = k_nb1; sa.nb2[0] = k_nb2; sa.nb3[0] = k_nb3;
+    sa.nb1[1] = v_nb1; sa.nb2[1] = v_nb2; sa.nb3[1] = v_nb3;
+    sa.dst[0] = dk; sa.dst[1] = dv;
+    sa.total8 = (uint32_t)total8;
+    uint32_t l2 = 0;
+    while ((1 << l2) < d / 8) ++l2;
+    sa.c8_log2 = l2;
+    sa.h = DivMod::make((uint32_t)h);
+    sa.n = DivMod::make((uint32_t)n);
+    const dim3 grid((unsigned)((total8 + 255) / 256), 2);
+    hipLaunchKernelGGL(to_f16_kv_kernel, grid, dim3(256), 0, st, sa);
     return hipGetLastError();
 }
 

@@ -5,13 +5,21 @@
 // Replaces the backend kernel of GGML_OP_FLASH_ATTN_EXT for the encoder
 // calls of voxtral.cpp (src/voxtral.cpp:1580-1613, FA at :1611): the offline
 // encoder (hd 64, 20 heads, 1500 frames, bidirectional, mask = null, scale
-// 1/sqrt(64)) and, with MM = 2, the same op under an implicit causal /
-// window mask: the realtime encoder's sliding-causal window of 750
-// (src/voxtral.cpp:2179-2190; 32 heads).
+// 1/sqrt(64)) and the same op under a mask: the realtime encoder's
+// sliding-causal window of 750 (src/voxtral.cpp:2179-2190, the mask tensor
+// of :1564; 32 heads), as that F16 tensor (MM = 1) or as an implicit mask
+// (MM = 2).
 //
-// Masks (MM = 2): query row i attends kv j iff i + off - W < j <= i + off
-// (W = 0: no lower bound). A workgroup's KV groups split only the blocks
-// live for some of its 128 rows (at 1500 frames and W = 750 about 28 of the
+// Masks. MM = 2, an implicit mask: query row i attends kv j iff
+// i + off - W < j <= i + off (W = 0: no lower bound). MM = 1, an F16 mask
+// tensor: a pre-pass launch (mask_rows_kernel) records each mask row's live
+// interval [lo, hi] when the row is 0 on it and -inf elsewhere, as the
+// realtime encoder's window rows are; a workgroup whose rows all have one
+// then runs exactly the MM = 2 path with per-row bounds (the same bits as
+// the implicit mask). A workgroup with any other row (finite non-zero
+// entries, holes) walks every block and adds each score's mask value,
+// loaded per element: correct for any mask, and slow. A workgroup's KV
+// groups split only the blocks live for some of its 128 rows (at 1500 frames and W = 750 about 28 of the
 // 47 blocks), so dead blocks are never copied or computed. A block that is
 // not wholly live for all 32 rows of a half gets its dead scores set to
 // -inf, in a uniform branch at the top of the half that consumes its S (the
@@ -146,9 +154,74 @@ __device__ __forceinline__ void wait_blocks(int k) {
     }
 }
 
+// min / max over the 64 lanes (every lane gets the result)
+__device__ __forceinline__ int wave_min_i(int x) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) x = min(x, __shfl_xor(x, m, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) x = max(x, __shfl_xor(x, m, 64));
+    return x;
+}
+
+// The pre-pass of a mask tensor: one wavefront per mask row w = (batch bm_i,
+// plane p, row q), w = (bm_i * hm + p) * nq + q, writes out[w] = {lo, hi} when
+// the row's entries are 0 (+0 or -0) on [lo, hi] and -inf elsewhere, {n, -1}
+// when every entry is -inf, {-2, -2} otherwise. The row is read as the
+// 16-byte-aligned chunks that cover it (any row alignment; a chunk holds at
+// least one byte of the row, so it lies in the same granule as mask data),
+// entries outside the row dropped in registers; a second pass over the same
+// chunks looks for -inf entries inside [lo, hi].
+__global__ __launch_bounds__(256) void mask_rows_kernel(const uint16_t* mask, int64_t nb1, int64_t nb2, int64_t nb3,
+                                                        int n, int nq, int hm, int nrows, int2* out) {
+    const int lane = threadIdx.x & 63;
+    const int w = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (w >= nrows) return;   // the whole wavefront
+    const int q = w % nq, pb = w / nq, p = pb % hm, bb = pb / hm;
+    const char* rowp = (const char*)mask + (int64_t)q * nb1 + (int64_t)p * nb2 + (int64_t)bb * nb3;
+    const int mis = (int)(reinterpret_cast<uintptr_t>(rowp) & 15);   // even: the mask is 2-byte aligned
+    const char* base = rowp - mis;
+    const int nch = (mis + 2 * n + 15) / 16;
+    int lo = 0x7fffffff, hi = -1;
+    bool nonzero = false;
+    for (int c = lane; c < nch; c += 64) {
+        const u32x4 wv = *(const u32x4*)(base + 16 * c);
+        const int col0 = (16 * c - mis) / 2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int col = col0 + e;
+            const uint32_t v = (wv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+            if (col < 0 || col >= n || v == kF16NegInf) continue;
+            lo = min(lo, col);
+            hi = max(hi, col);
+            nonzero = nonzero || (v & 0x7FFFu) != 0;
+        }
+    }
+    lo = wave_min_i(lo);
+    hi = wave_max_i(hi);
+    nonzero = __any(nonzero);
+    bool hole = false;
+    if (!nonzero && hi >= lo) {
+        for (int c = lane; c < nch; c += 64) {
+            const u32x4 wv = *(const u32x4*)(base + 16 * c);
+            const int col0 = (16 * c - mis) / 2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = col0 + e;
+                const uint32_t v = (wv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                hole = hole || (col > lo && col < hi && v == kF16NegInf);
+            }
+        }
+        hole = __any(hole);
+    }
+    if (lane == 0) out[w] = (nonzero || hole) ? int2{-2, -2} : (hi < lo ? int2{n, -1} : int2{lo, hi});
+}
+
 template <bool QF16, bool C8, int MM>
 __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm, int nblk, int ni) {
-    static_assert(MM == 0 || MM == 2, "no mask, or an implicit causal / window mask");
+    static_assert(MM == 0 || MM == 1 || MM == 2, "no mask, a mask tensor, or an implicit causal / window mask");
     using namespace pp;
     static_assert(NLD * NQT == 4, "a block's 4 load instructions per matrix split evenly");
     static_assert(8 * 2 * NLD < 64 && NS <= 8, "vmcnt range of wait_blocks");
@@ -171,22 +244,17 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
 
-    // blocks [blo, blo + nblk) hold the live KV positions of the workgroup's
-    // rows (all of them without a mask); KV group kg takes [bs, bs + ng)
-    int blo = 0;
-    if constexpr (MM == 2) {
-        const int64_t q1 = min(qw0 + BM, a.nq) - 1;      // the workgroup's last real row
-        int64_t lo = a.im_window > 0 ? (int64_t)qw0 + a.im_offset - a.im_window + 1 : 0;
-        int64_t hi = q1 + a.im_offset + 1;                // exclusive
-        lo = lo < 0 ? 0 : lo;
-        hi = hi > a.nkv ? a.nkv : hi;
-        if (hi <= lo) lo = hi = 0;
-        blo = (int)(lo / BK);
-        nblk = (int)((hi + BK - 1) / BK) - blo;
-        ni = (nblk + KVG - 1) / KVG;
+    // MM = 1: the live intervals of the lane's rows in the two halves (loaded
+    // before Q, so that their wait leaves the Q loads in flight)
+    int2 ivl[2] = {int2{0, 0}, int2{0, 0}};
+    if constexpr (MM == 1) {
+        const int2* tab = a.mask_rows + ((int64_t)(b % a.bm) * a.hm + (h % a.hm)) * a.nq;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int row = qw0 + 64 * wq + 32 * x + nl;
+            ivl[x] = row < a.nq ? tab[row] : int2{a.nkv, -1};
+        }
     }
-    const int bs = blo + min(kg * ni, nblk);
-    const int ng = min(ni, blo + nblk - bs);
 
     // ---- Q: coalesced loads by the whole workgroup (issued first, so their
     // latency overlaps the first K/V blocks) -----------------------------------
@@ -208,6 +276,66 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
             qraw[u] = __builtin_nontemporal_load((const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 +
                                                                   (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3 + cch * 16));
     }
+
+    // MM = 1: whether every row of the workgroup has a live interval (mslow
+    // = false) and the union of the intervals, reduced over both query tiles
+    // through LDS
+    bool mslow = false;
+    int wlo = 0x7fffffff, whi = -1;
+    if constexpr (MM == 1) {
+        __shared__ int xg[NQT][3];
+        bool non = false;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            non = non || ivl[x].x == -2;
+            if (ivl[x].x >= 0 && ivl[x].x <= ivl[x].y) {
+                wlo = min(wlo, ivl[x].x);
+                whi = max(whi, ivl[x].y);
+            }
+        }
+        wlo = wave_min_i(wlo);
+        whi = wave_max_i(whi);
+        non = __any(non);
+        if (kg == 0 && lane == 0) {
+            xg[wq][0] = wlo;
+            xg[wq][1] = whi;
+            xg[wq][2] = non ? 1 : 0;
+        }
+        __syncthreads();
+        // (uniform: scalar registers, so the loop bounds stay scalar)
+        wlo = __builtin_amdgcn_readfirstlane(min(xg[0][0], xg[NQT - 1][0]));
+        whi = __builtin_amdgcn_readfirstlane(max(xg[0][1], xg[NQT - 1][1]));
+        mslow = __builtin_amdgcn_readfirstlane(xg[0][2] | xg[NQT - 1][2]) != 0;
+    }
+    // blocks [blo, blo + nblk) hold the live KV positions of the workgroup's
+    // rows (all of them without a mask, or with mslow);
+    // KV group kg takes [bs, bs + ng)
+    int blo = 0;
+    if constexpr (MM == 1) {
+        if (!mslow) {
+            if (whi < wlo) {
+                nblk = 0;
+            } else {
+                blo = wlo / BK;
+                nblk = (whi + BK) / BK - blo;
+            }
+            ni = (nblk + KVG - 1) / KVG;
+        }
+    }
+    if constexpr (MM == 2) {
+        const int64_t q1 = min(qw0 + BM, a.nq) - 1;      // the workgroup's last real row
+        int64_t lo = a.im_window > 0 ? (int64_t)qw0 + a.im_offset - a.im_window + 1 : 0;
+        int64_t hi = q1 + a.im_offset + 1;                // exclusive
+        lo = lo < 0 ? 0 : lo;
+        hi = hi > a.nkv ? a.nkv : hi;
+        if (hi <= lo) lo = hi = 0;
+        blo = (int)(lo / BK);
+        nblk = (int)((hi + BK - 1) / BK) - blo;
+        ni = (nblk + KVG - 1) / KVG;
+    }
+    const int bs = blo + min(kg * ni, nblk);
+    const int ng = min(ni, blo + nblk - bs);
+
 
     // ---- block loads: global -> LDS ring -------------------------------------
     // Instruction i of wavefront wq fills rows [8 (NQT i + wq), + 8) of the
@@ -338,11 +466,21 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         for (int j = 0; j < 16; ++j)
             if (kv0 + pf_kv_of(hh, j) >= a.nkv) sc[j] = -INFINITY;
     };
-    // MM = 2: the live positions [rlo, rhi] of the lane's row in each half
-    // (clamped to [-1, n_kv]), and per half the largest lower bound and the
-    // smallest upper bound over its 32 rows (a block inside both is wholly
-    // live for the half)
+    // MM = 1 / 2: the live positions [rlo, rhi] of the lane's row in each
+    // half (clamped to [-1, n_kv]), and per half the largest lower bound and
+    // the smallest upper bound over its 32 rows (a block inside both is
+    // wholly live for the half)
     int rlo[2] = {0, 0}, rhi[2] = {0, 0}, hlo[2] = {0, 0}, hhi[2] = {0, 0};
+    if constexpr (MM == 1) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            rlo[x] = ivl[x].x;
+            rhi[x] = ivl[x].y;
+            // (lanes l and l + 32 hold the same row; uniform results)
+            hlo[x] = __builtin_amdgcn_readfirstlane(wave_max_i(rlo[x]));
+            hhi[x] = __builtin_amdgcn_readfirstlane(wave_min_i(rhi[x]));
+        }
+    }
     if constexpr (MM == 2) {
         auto clampkv = [&](int64_t x) { return (int)(x < -1 ? -1 : (x > a.nkv ? a.nkv : x)); };
 #pragma unroll
@@ -355,10 +493,36 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
             hhi[x] = clampkv(r0 + a.im_offset);
         }
     }
-    // MM = 2: block blk (of this group) for half x; a uniform branch, taken
-    // only for blocks not wholly live for the half's rows
+    // MM = 1 / 2: block blk (of this group) for half x; a uniform branch,
+    // taken only for blocks not wholly live for the half's rows. MM = 1,
+    // mslow: every score gets its mask value (per element loads; -inf, and
+    // a position past n_kv, remove it; a finite value m adds m / |scale|,
+    // so that c s becomes c s + m log2(e)). The lane's mask row (rows past
+    // n_q read row n_q - 1; their outputs are not stored) is addressed here
+    // rather than held in registers across the loop (the empty asm keeps
+    // the computation here).
     auto mask_fix = [&](floatx16& sc, int blk, int x) {
-        if constexpr (MM == 2) {
+        if constexpr (MM == 1) {
+            if (mslow) {
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const int row = min(qw0 + 64 * wq + 32 * x + (ln & 31), a.nq - 1);
+                const uint16_t* mr = (const uint16_t*)((const char*)a.mask + (int64_t)(h % a.hm) * a.m_nb2 +
+                                                       (int64_t)(b % a.bm) * a.m_nb3 + (int64_t)row * a.m_nb1);
+                const int kv0 = (bs + blk) * BK;
+                const float inv_sc = kLog2e / c;
+                uint16_t mv[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) mv[j] = mr[min(kv0 + pf_kv_of(ln >> 5, j), a.nkv - 1)];
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    sc[j] = (mv[j] == kF16NegInf || kv0 + pf_kv_of(ln >> 5, j) >= a.nkv)
+                                ? -INFINITY
+                                : fmaf(f16_bits_to_f32(mv[j]), inv_sc, sc[j]);
+                return;
+            }
+        }
+        if constexpr (MM != 0) {
             const int kv0 = (bs + blk) * BK;
             if (!(kv0 >= hlo[x] && kv0 + BK - 1 <= hhi[x])) {
 #pragma unroll
@@ -414,10 +578,18 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         l *= alpha;
         m = mnew;
     };
+    // With a mask, rows past n_q (their outputs are not stored) take no part
+    // in the wavefront's choice of the exact path: its rows then see the same
+    // choices under any two masks that agree on the real rows (an implicit
+    // mask and the same mask as a tensor give the same bits). Such a row may
+    // keep m = -inf and turn its own P, l and O to inf / NaN; each row's
+    // values stay in its own column of P and O and are dropped at the store.
+    const bool real_a = MM == 0 || qw0 + 64 * wq + nl < a.nq;
+    const bool real_b = MM == 0 || qw0 + 64 * wq + 32 + nl < a.nq;
     // softmax of one block, max first (blocks outside the pipelined loop)
-    auto softmax_exact = [&](const floatx16& sc, float& m, float& l, floatx16 (&o)[DB], half8 (&p)[2]) {
+    auto softmax_exact = [&](const floatx16& sc, float& m, float& l, floatx16 (&o)[DB], half8 (&p)[2], bool real) {
         const float mx = block_max(sc);
-        if (__any(mx > m + TAU)) raise(mx, m, l, o);
+        if (__any(mx > m + TAU && real)) raise(mx, m, l, o);
         l += exps(sc, m, p);
     };
     // Softmax inside the pipelined loop. P is computed against the current
@@ -434,7 +606,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     // MFMA per 5 VALU instructions; in H2 (operands in registers) one MFMA per
     // 6 from the start.
     auto softmax_spec = [&](auto half_tag, const floatx16& sc, float& m, float& l, floatx16 (&o)[DB],
-                            half8 (&p)[2]) {
+                            half8 (&p)[2], bool real) {
         constexpr int HALF = decltype(half_tag)::value;
         float ls = exps(sc, m, p);
         if constexpr (HALF == 1) {
@@ -455,7 +627,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         // 2^TAU (also true for inf / NaN); with a mask, also a row that has
         // no live score yet (its P above were taken against m = 0)
         bool slow = !(ls <= 256.0f);
-        if constexpr (MM != 0) slow = slow || m == -INFINITY;
+        if constexpr (MM != 0) slow = (slow || m == -INFINITY) && real;
         if (__any(slow)) {
             raise(block_max(sc), m, l, o);
             ls = exps(sc, m, p);
@@ -498,7 +670,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         s_mfma(sb, qb, kr);
         mask_fix(sa, 0, 0);
         mask_fix(sb, 0, 1);
-        softmax_exact(sa, ma, la, oa, pa);
+        softmax_exact(sa, ma, la, oa, pa, real_a);
         // the loop's softmax needs a finite running max to start from
         mb = block_max(sb);
     }
@@ -523,14 +695,14 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         // operands are in registers while K_{t+1} lands.
         pv_mfma(oa, pa, vr);
         s_mfma(sa, qa, kr);
-        softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb);
+        softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb, real_b);
         if ((t == 0 ? NS - 1 : t + NS) < ng) issue(t == 0 ? NS - 1 : t + NS);
         // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
         mask_fix(sa, t + 1, 0);
         pv_mfma(ob, pb, vr);
         read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
         s_mfma(sb, qb, kr);
-        softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa);
+        softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa, real_a);
         // blocks issued so far: up to NS - 1 (t = 0), t + NS (t >= 1)
         const int last = min(t >= 1 ? t + NS : NS - 1, ng - 1);
         wait_blocks_loop<NLD>(last - (t + 2));   // 2 at most: last <= t + NS
@@ -541,7 +713,7 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         // last full block: PV_A, softmax of S_B, PV_B
         if (nf > 1) mask_fix(sb, nf - 1, 1);
         pv_mfma(oa, pa, vr);
-        softmax_exact(sb, mb, lb, ob, pb);
+        softmax_exact(sb, mb, lb, ob, pb, real_b);
         pv_mfma(ob, pb, vr);
         wait_vmcnt<0>();
         __syncthreads();
@@ -557,8 +729,8 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         tail_fix(sb, tp);
         mask_fix(sa, tp, 0);
         mask_fix(sb, tp, 1);
-        softmax_exact(sa, ma, la, oa, pa);
-        softmax_exact(sb, mb, lb, ob, pb);
+        softmax_exact(sa, ma, la, oa, pa, real_a);
+        softmax_exact(sb, mb, lb, ob, pb, real_b);
         pv_mfma(oa, pa, vr);
         pv_mfma(ob, pb, vr);
         __syncthreads();
@@ -683,9 +855,18 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
     const bool is_c8 = fabsf(a.scale_log2) == c8 && __builtin_bit_cast(uint32_t, c8) == 0x3e38aa3bu;
     const GridMap gm = GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
-    if (a.mask) return hipErrorInvalidValue;
-    if (a.im_causal) launch_pp_mm<2>(a, gm, nblk, ni, is_c8, grid, block, st);
-    else launch_pp_mm<0>(a, gm, nblk, ni, is_c8, grid, block, st);
+    if (a.mask) {
+        if (!a.mask_rows) return hipErrorInvalidValue;
+        const int64_t nrows = (int64_t)a.nq * a.hm * a.bm;
+        if (nrows > 0x7fffffff - 3) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(mask_rows_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, a.mask, a.m_nb1,
+                           a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows);
+        launch_pp_mm<1>(a, gm, nblk, ni, is_c8, grid, block, st);
+    } else if (a.im_causal) {
+        launch_pp_mm<2>(a, gm, nblk, ni, is_c8, grid, block, st);
+    } else {
+        launch_pp_mm<0>(a, gm, nblk, ni, is_c8, grid, block, st);
+    }
     return hipGetLastError();
 }
 

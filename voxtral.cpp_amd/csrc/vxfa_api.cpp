@@ -32,7 +32,7 @@ constexpr size_t kStageBytes = (size_t)32 << 20;        // F32 K and V of 8192 r
 struct Tuning {
     int split_override = 0;
     int waves_override = 0;
-    // VXFA_PREFILL_PP=0 routes hd 64 unmasked prefill to the general kernel
+    // VXFA_PREFILL_PP=0 routes hd 64 prefill to the general kernel
     bool pp_enabled = true;
     // VXFA_PREFILL_PAIR=0 routes short masked hd 128 prefill to the general kernel
     bool pair_enabled = true;
@@ -484,6 +484,7 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
         a.ws = w.rec;
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
+        size_t staged = 0;   // bytes of the staging area this call fills
         if (a.kv_f32) {
             // F32 K/V (the reference's own cache and encoder K/V): an f16 copy
             // in the context's staging area, [Bk][Nkv][Hkv][D], read by the
@@ -498,12 +499,12 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             }
             _Float16* sk = w.stage;
             _Float16* sv = w.stage + per;
-            e = vxfa::launch_to_f16(static_cast<const float*>(k->data), (int64_t)k->nb[1], (int64_t)k->nb[2],
-                                    (int64_t)k->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sk, st);
-            if (e == hipSuccess)
-                e = vxfa::launch_to_f16(static_cast<const float*>(v->data), (int64_t)v->nb[1], (int64_t)v->nb[2],
-                                        (int64_t)v->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sv, st);
+            e = vxfa::launch_to_f16_kv(static_cast<const float*>(k->data), (int64_t)k->nb[1], (int64_t)k->nb[2],
+                                       (int64_t)k->nb[3], static_cast<const float*>(v->data), (int64_t)v->nb[1],
+                                       (int64_t)v->nb[2], (int64_t)v->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sk,
+                                       sv, st);
             if (e != hipSuccess) { set_err(w, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+            staged = (size_t)(2 * per) * sizeof(_Float16);
             a.k = sk;
             a.v = sv;
             a.k_nb1 = a.v_nb1 = Hkv * D * 2;
@@ -511,11 +512,25 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             a.k_nb3 = a.v_nb3 = Nkv * Hkv * D * 2;
             a.kv_f32 = 0;
         }
-        if (D == 64 && !mask && !rope && scale != 0.0f && w.tune.pp_enabled) {
+        // a mask tensor on the pipelined hd 64 kernel: the live interval of
+        // each mask row (8 bytes a row) in the records region, unused by a
+        // prefill call; where records and staging share one area (the no-alloc
+        // scratch), after the staged K/V
+        bool pp_mask_fits = false;
+        if (mask) {
+            const size_t off = w.rec == reinterpret_cast<float*>(w.stage) ? (staged + 255) & ~(size_t)255 : 0;
+            const size_t need = (size_t)(Nq * a.hm * a.bm) * sizeof(int2);
+            if (off + need <= w.rec_bytes) {
+                a.mask_rows = reinterpret_cast<int2*>(reinterpret_cast<char*>(w.rec) + off);
+                pp_mask_fits = true;
+            }
+        }
+        if (D == 64 && (!mask || pp_mask_fits) && !rope && scale != 0.0f && w.tune.pp_enabled) {
             // (scale 0 goes to the general kernel: the pipelined one folds the
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel, also under
-            // an implicit causal / window mask (the realtime encoder's window)
+            // an implicit causal / window mask or a mask tensor (the realtime
+            // encoder's window)
             e = vxfa::launch_prefill64_pp(a, st);
         } else if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled && vxfa::prefill_pair_fits(a)) {
             // short masked prefill (voxtral's decoder prefill): paired query
