@@ -147,31 +147,50 @@ NEG_INF_F16 = 0xFC00
 def mask_row_interval(row, mis):
     """The pre-pass of a mask tensor (mask_rows_kernel) for one F16 mask row
     (uint16 array of n entries) whose first entry sits mis bytes (even, < 16)
-    past a 16-byte boundary: the kernel reads 16-byte chunks c = 0 .. nch - 1
-    from the boundary, entry e of chunk c being column (16 c - mis) / 2 + e,
-    drops the columns outside [0, n), and returns (lo, hi) when the row is
-    +-0 on [lo, hi] and -inf elsewhere, (n, -1) when every entry is -inf,
-    (-2, -2) otherwise."""
+    past a 16-byte boundary: 16 lanes read 16-byte chunks from the boundary,
+    lane s of round c0 (c0 = 0, 192, ... below nchmax, the chunk count of the
+    worst alignment) chunk min(c0 + 16 u + s, nch - 1) for u < 12, entry e
+    of chunk slot c being column 8 c - mis / 2 + e; the entries of
+    [elo, ehi) (those in [0, n)) count, through bit masks: live (in the row,
+    not -inf) and nz (live and non-zero). From the first and last live
+    columns lo and hi, their count and whether one is non-zero it returns
+    (lo, hi) when the row is +-0 on [lo, hi] and -inf elsewhere (count
+    hi - lo + 1, none non-zero), (n, -1) when every entry is -inf, (-2, -2)
+    otherwise."""
     n = len(row)
     nch = (mis + 2 * n + 15) // 16
-    lo, hi, nonzero = 1 << 31, -1, False
-    cols = []
-    for c in range(nch):
-        for e in range(8):
-            col = (16 * c - mis) // 2 + e
-            cols.append(col)
-            if col < 0 or col >= n or row[col] == NEG_INF_F16:
-                continue
-            lo, hi = min(lo, col), max(hi, col)
-            nonzero = nonzero or (int(row[col]) & 0x7FFF) != 0
-    _check(sorted(c for c in cols if 0 <= c < n) == list(range(n)), "the chunks miss or repeat a column")
-    _check(all(-8 <= c < n + 8 for c in cols), "a chunk lies wholly outside the row")
-    hole = False
-    if not nonzero and hi >= lo:
-        hole = any(lo < c < hi and row[c] == NEG_INF_F16 for c in cols if 0 <= c < n)
-    if nonzero or hole:
-        return (-2, -2)
-    return (n, -1) if hi < lo else (lo, hi)
+    nchmax = (14 + 2 * n + 15) // 16
+    _check(nch <= nchmax, "the row has more chunks than the loop walks")
+    lo, hi, cnt, nonzero = 1 << 31, -1, 0, False
+    counted = []
+    for c0 in range(0, nchmax, 16 * 12):
+        for u in range(12):
+            for s in range(16):
+                c = c0 + 16 * u + s
+                ld = min(c, nch - 1)             # the chunk the lane loads
+                _check(0 <= ld < nch, "a load outside the row's chunks")
+                col0 = 8 * c - mis // 2
+                elo, ehi = max(-col0, 0), min(n - col0, 8)
+                valid = ((1 << ehi) - 1) & ~((1 << elo) - 1) if ehi > elo else 0
+                _check(c == ld or valid == 0, "a reloaded chunk counts")
+                live = nz = 0
+                for e in range(8):
+                    if not (valid >> e) & 1:
+                        continue
+                    v = int(row[col0 + e])
+                    l = v != NEG_INF_F16
+                    live |= l << e
+                    nz |= (l and (v & 0x7FFF) != 0) << e
+                    counted.append(col0 + e)
+                nonzero = nonzero or nz != 0
+                if live:
+                    first = col0 + (live & -live).bit_length() - 1
+                    last = col0 + live.bit_length() - 1
+                    lo, hi, cnt = min(lo, first), max(hi, last), cnt + bin(live).count("1")
+    _check(sorted(counted) == list(range(n)), "the chunks miss or repeat a column")
+    if hi < lo:
+        return (n, -1)
+    return (-2, -2) if nonzero or cnt != hi - lo + 1 else (lo, hi)
 
 
 def pp_block_range_table(sh: Shape, qg, table, BM=128):

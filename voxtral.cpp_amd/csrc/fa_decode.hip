@@ -766,26 +766,38 @@ struct StageArgs {
     DivMod h, n;
 };
 
+// Each thread converts kStageUnits groups of 8 elements, 256 groups apart
+// (2 x kStageUnits 16-byte loads in flight per thread).
+constexpr int kStageUnits = 4;
 __global__ __launch_bounds__(256) void to_f16_kv_kernel(StageArgs sa) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= sa.total8) return;
     const int t = blockIdx.y;
-    const uint32_t r = i >> sa.c8_log2;                  // row index (b, pos, h)
-    const uint32_t e = (i - (r << sa.c8_log2)) * 8;      // first element in the row
-    const uint32_t r2 = sa.h.div(r);
-    const uint32_t hh = r - r2 * sa.h.d;
-    const uint32_t bb = sa.n.div(r2);
-    const uint32_t pos = r2 - bb * sa.n.d;
-    const floatx4* p = (const floatx4*)((const char*)sa.src[t] + (int64_t)pos * sa.nb1[t] + (int64_t)hh * sa.nb2[t] +
-                                        (int64_t)bb * sa.nb3[t]) + e / 4;
-    const floatx4 x0 = __builtin_nontemporal_load(p), x1 = __builtin_nontemporal_load(p + 1);
-    half8 y;
+    const uint32_t i0 = blockIdx.x * (256u * kStageUnits) + threadIdx.x;
+    floatx4 x[kStageUnits][2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        y[j] = (_Float16)x0[j];
-        y[4 + j] = (_Float16)x1[j];
+    for (int u = 0; u < kStageUnits; ++u) {
+        const uint32_t i = min(i0 + 256u * u, sa.total8 - 1);   // past the end: reload the last group, store nothing
+        const uint32_t r = i >> sa.c8_log2;                     // row index (b, pos, h)
+        const uint32_t e = (i - (r << sa.c8_log2)) * 8;         // first element in the row
+        const uint32_t r2 = sa.h.div(r);
+        const uint32_t hh = r - r2 * sa.h.d;
+        const uint32_t bb = sa.n.div(r2);
+        const uint32_t pos = r2 - bb * sa.n.d;
+        const floatx4* p = (const floatx4*)((const char*)sa.src[t] + (int64_t)pos * sa.nb1[t] +
+                                            (int64_t)hh * sa.nb2[t] + (int64_t)bb * sa.nb3[t]) + e / 4;
+        x[u][0] = __builtin_nontemporal_load(p);
+        x[u][1] = __builtin_nontemporal_load(p + 1);
     }
-    *(half8*)(sa.dst[t] + (int64_t)i * 8) = y;
+#pragma unroll
+    for (int u = 0; u < kStageUnits; ++u) {
+        const uint32_t i = i0 + 256u * u;
+        half8 y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            y[j] = (_Float16)x[u][0][j];
+            y[4 + j] = (_Float16)x[u][1][j];
+        }
+        if (i < sa.total8) *(half8*)(sa.dst[t] + (int64_t)i * 8) = y;
+    }
 }
 
 hipError_t launch_to_f16_kv(const float* k, int64_t k_nb1, int64_t k_nb2, int64_t k_nb3, const float* v, int64_t v_nb1,
@@ -806,7 +818,7 @@ hipError_t launch_to_f16_kv(const float* k, int64_t k_nb1, int64_t k_nb2, int64_
     sa.c8_log2 = l2;
     sa.h = DivMod::make((uint32_t)h);
     sa.n = DivMod::make((uint32_t)n);
-    const dim3 grid((unsigned)((total8 + 255) / 256), 2);
+    const dim3 grid((unsigned)((total8 + 256 * kStageUnits - 1) / (256 * kStageUnits)), 2);
     hipLaunchKernelGGL(to_f16_kv_kernel, grid, dim3(256), 0, st, sa);
     return hipGetLastError();
 }

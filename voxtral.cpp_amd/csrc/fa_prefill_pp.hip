@@ -166,57 +166,87 @@ __device__ __forceinline__ int wave_max_i(int x) {
     return x;
 }
 
-// The pre-pass of a mask tensor: one wavefront per mask row w = (batch bm_i,
-// plane p, row q), w = (bm_i * hm + p) * nq + q, writes out[w] = {lo, hi} when
-// the row's entries are 0 (+0 or -0) on [lo, hi] and -inf elsewhere, {n, -1}
-// when every entry is -inf, {-2, -2} otherwise. The row is read as the
-// 16-byte-aligned chunks that cover it (any row alignment; a chunk holds at
-// least one byte of the row, so it lies in the same granule as mask data),
-// entries outside the row dropped in registers; a second pass over the same
-// chunks looks for -inf entries inside [lo, hi].
-__global__ __launch_bounds__(256) void mask_rows_kernel(const uint16_t* mask, int64_t nb1, int64_t nb2, int64_t nb3,
-                                                        int n, int nq, int hm, int nrows, int2* out) {
-    const int lane = threadIdx.x & 63;
-    const int w = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-    if (w >= nrows) return;   // the whole wavefront
-    const int q = w % nq, pb = w / nq, p = pb % hm, bb = pb / hm;
+// min / max / sum over the 16 lanes of a DPP row (every lane of the row gets
+// the result; row rotates are VALU operand modifiers, no LDS traffic)
+__device__ __forceinline__ int row16_min_i(int x) {
+    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x122, 0xF, 0xF, false));
+    return min(x, __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int row16_max_i(int x) {
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x122, 0xF, 0xF, false));
+    return max(x, __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int row16_sum_i(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x122, 0xF, 0xF, false);
+    return x + __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false);
+}
+
+// The pre-pass of a mask tensor: 16 lanes (one DPP row) per mask row
+// w = (batch bm_i, plane p, row q), w = (bm_i * hm + p) * nq + q, 4 rows per
+// single-wavefront workgroup; writes out[w] = {lo, hi} when the row's entries
+// are 0 (+0 or -0) on [lo, hi] and -inf elsewhere, {n, -1} when every entry
+// is -inf, {-2, -2} otherwise. The row is read as the 16-byte-aligned chunks
+// that cover it (any row alignment; a chunk holds at least one byte of the
+// row, so it lies in the same granule as mask data): in rounds of 192
+// chunks, lane s of the row loading chunks c0 + 16 u + s (u < 12, all in
+// flight; a chunk past the row's last reloads the last and counts nothing).
+// Branch-free per chunk: bit e of `live` is set when entry e lies in the row
+// and is not -inf, of `nz` when it is also non-zero; one pass gives the first
+// and last live column, their count and whether one is non-zero (the row is
+// an interval iff the count is hi - lo + 1), reduced over the row's 16 lanes
+// with DPP rotates.
+constexpr int kMaskRowChunks = 12;   // chunks per lane per round
+__global__ __launch_bounds__(64) void mask_rows_kernel(const uint16_t* mask, int64_t nb1, int64_t nb2, int64_t nb3,
+                                                       int n, int nq, int hm, int nrows, int2* out) {
+    const int s = threadIdx.x & 15;
+    const int w = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 4);
+    const int wr = min(w, nrows - 1);   // a row group past the last row reads the last row, writes nothing
+    const int q = wr % nq, pb = wr / nq, p = pb % hm, bb = pb / hm;
     const char* rowp = (const char*)mask + (int64_t)q * nb1 + (int64_t)p * nb2 + (int64_t)bb * nb3;
     const int mis = (int)(reinterpret_cast<uintptr_t>(rowp) & 15);   // even: the mask is 2-byte aligned
     const char* base = rowp - mis;
     const int nch = (mis + 2 * n + 15) / 16;
-    int lo = 0x7fffffff, hi = -1;
-    bool nonzero = false;
-    for (int c = lane; c < nch; c += 64) {
-        const u32x4 wv = *(const u32x4*)(base + 16 * c);
-        const int col0 = (16 * c - mis) / 2;
+    const int nchmax = (14 + 2 * n + 15) / 16;                         // the same loop for every row
+    int lo = 0x7fffffff, hi = -1, cnt = 0;
+    uint32_t nzall = 0;
+    for (int c0 = 0; c0 < nchmax; c0 += 16 * kMaskRowChunks) {
+        u32x4 wv[kMaskRowChunks];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int col = col0 + e;
-            const uint32_t v = (wv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-            if (col < 0 || col >= n || v == kF16NegInf) continue;
-            lo = min(lo, col);
-            hi = max(hi, col);
-            nonzero = nonzero || (v & 0x7FFFu) != 0;
-        }
-    }
-    lo = wave_min_i(lo);
-    hi = wave_max_i(hi);
-    nonzero = __any(nonzero);
-    bool hole = false;
-    if (!nonzero && hi >= lo) {
-        for (int c = lane; c < nch; c += 64) {
-            const u32x4 wv = *(const u32x4*)(base + 16 * c);
-            const int col0 = (16 * c - mis) / 2;
+        for (int u = 0; u < kMaskRowChunks; ++u) wv[u] = *(const u32x4*)(base + 16 * min(c0 + 16 * u + s, nch - 1));
+#pragma unroll
+        for (int u = 0; u < kMaskRowChunks; ++u) {
+            const int col0 = 8 * (c0 + 16 * u + s) - mis / 2;      // column of the chunk's first entry
+            const int elo = max(-col0, 0), ehi = min(n - col0, 8);  // entries [elo, ehi) lie in the row
+            const uint32_t valid = ehi > elo ? ((1u << ehi) - 1u) & ~((1u << elo) - 1u) : 0u;
+            uint32_t live = 0, nz = 0;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int col = col0 + e;
-                const uint32_t v = (wv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-                hole = hole || (col > lo && col < hi && v == kF16NegInf);
+                const uint32_t v = (wv[u][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                const uint32_t l = v != kF16NegInf ? 1u : 0u;
+                live |= l << e;
+                nz |= (l & ((v & 0x7FFFu) != 0 ? 1u : 0u)) << e;
             }
+            live &= valid;
+            nzall |= nz & valid;
+            const int first = col0 + (int)__builtin_ctz(live | 0x100u);
+            const int last = col0 + 31 - (int)__builtin_clz(live | 1u);
+            lo = live ? min(lo, first) : lo;
+            hi = live ? max(hi, last) : hi;
+            cnt += __builtin_popcount(live);
         }
-        hole = __any(hole);
     }
-    if (lane == 0) out[w] = (nonzero || hole) ? int2{-2, -2} : (hi < lo ? int2{n, -1} : int2{lo, hi});
+    lo = row16_min_i(lo);
+    hi = row16_max_i(hi);
+    cnt = row16_sum_i(cnt);
+    const int nonzero = row16_max_i(nzall != 0 ? 1 : 0);
+    if (s == 0 && w < nrows)
+        out[w] = hi < lo ? int2{n, -1} : ((nonzero || cnt != hi - lo + 1) ? int2{-2, -2} : int2{lo, hi});
 }
 
 template <bool QF16, bool C8, int MM>
@@ -244,16 +274,16 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     const char* kb = (const char*)a.k + (int64_t)hk * a.k_nb2 + (int64_t)bkv * a.k_nb3;
     const char* vb = (const char*)a.v + (int64_t)hk * a.v_nb2 + (int64_t)bkv * a.v_nb3;
 
-    // MM = 1: the live intervals of the lane's rows in the two halves (loaded
-    // before Q, so that their wait leaves the Q loads in flight)
-    int2 ivl[2] = {int2{0, 0}, int2{0, 0}};
+    // MM = 1: the intervals of the workgroup's 128 rows, rows l and 64 + l on
+    // lane l (loaded before Q, so that their wait leaves the Q loads in
+    // flight; rows past n_q load row n_q - 1 and count as empty). Loads here
+    // are unconditional: a load under a branch makes the compiler wait for
+    // it at the join, before the K/V copies are issued.
+    int2 iv[2] = {int2{0, 0}, int2{0, 0}};
     if constexpr (MM == 1) {
         const int2* tab = a.mask_rows + ((int64_t)(b % a.bm) * a.hm + (h % a.hm)) * a.nq;
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            const int row = qw0 + 64 * wq + 32 * x + nl;
-            ivl[x] = row < a.nq ? tab[row] : int2{a.nkv, -1};
-        }
+        for (int u = 0; u < 2; ++u) iv[u] = tab[min(qw0 + 64 * u + lane, a.nq - 1)];
     }
 
     // ---- Q: coalesced loads by the whole workgroup (issued first, so their
@@ -263,6 +293,8 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     // the BM x 16 chunks; F16 Q: of the BM x 8 chunks.
     // Q is read once and O written once (whole 256-byte rows): nontemporal
     // loads and stores (21.7 -> 20.3 us per layer measured on one box).
+    // Rows past n_q load row n_q - 1 (unconditional loads, see above) and
+    // are staged as zeros.
     constexpr int QCH = QF16 ? 8 : 16;         // 16-byte global chunks per row
     constexpr int QPT = BM * QCH / NT;         // per thread
     floatx4 qraw[QPT];
@@ -270,42 +302,40 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
     for (int u = 0; u < QPT; ++u) {
         const int i = tid + NT * u;
         const int r = i / QCH, cch = i % QCH;
-        const int row = qw0 + r;
-        qraw[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (row < a.nq)
-            qraw[u] = __builtin_nontemporal_load((const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 +
-                                                                  (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3 + cch * 16));
+        const int row = min(qw0 + r, a.nq - 1);
+        qraw[u] = __builtin_nontemporal_load((const floatx4*)((const char*)a.q + (int64_t)row * a.q_nb1 +
+                                                              (int64_t)h * a.q_nb2 + (int64_t)b * a.q_nb3 + cch * 16));
     }
 
     // MM = 1: whether every row of the workgroup has a live interval (mslow
-    // = false) and the union of the intervals, reduced over both query tiles
-    // through LDS
+    // = false), the union of the intervals (uniform: scalar registers, so
+    // the loop bounds stay scalar; every wavefront reduces all 128 rows, no
+    // barrier), and the intervals of the lane's rows in the two halves
+    // (rows 64 wq + 32 x + l % 32)
     bool mslow = false;
     int wlo = 0x7fffffff, whi = -1;
+    int2 ivl[2] = {int2{0, 0}, int2{0, 0}};
     if constexpr (MM == 1) {
-        __shared__ int xg[NQT][3];
         bool non = false;
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            non = non || ivl[x].x == -2;
-            if (ivl[x].x >= 0 && ivl[x].x <= ivl[x].y) {
-                wlo = min(wlo, ivl[x].x);
-                whi = max(whi, ivl[x].y);
+        for (int u = 0; u < 2; ++u) {
+            if (qw0 + 64 * u + lane >= a.nq) iv[u] = int2{a.nkv, -1};
+            non = non || iv[u].x == -2;
+            if (iv[u].x >= 0 && iv[u].x <= iv[u].y) {
+                wlo = min(wlo, iv[u].x);
+                whi = max(whi, iv[u].y);
             }
         }
-        wlo = wave_min_i(wlo);
-        whi = wave_max_i(whi);
-        non = __any(non);
-        if (kg == 0 && lane == 0) {
-            xg[wq][0] = wlo;
-            xg[wq][1] = whi;
-            xg[wq][2] = non ? 1 : 0;
+        wlo = __builtin_amdgcn_readfirstlane(wave_min_i(wlo));
+        whi = __builtin_amdgcn_readfirstlane(wave_max_i(whi));
+        mslow = __any(non);
+        static_assert(NQT == 2, "a wavefront's 64 rows are iv[wq] of the workgroup's 128");
+        const int2 mine = wq ? iv[1] : iv[0];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            ivl[x].x = __shfl(mine.x, 32 * x + nl, 64);
+            ivl[x].y = __shfl(mine.y, 32 * x + nl, 64);
         }
-        __syncthreads();
-        // (uniform: scalar registers, so the loop bounds stay scalar)
-        wlo = __builtin_amdgcn_readfirstlane(min(xg[0][0], xg[NQT - 1][0]));
-        whi = __builtin_amdgcn_readfirstlane(max(xg[0][1], xg[NQT - 1][1]));
-        mslow = __builtin_amdgcn_readfirstlane(xg[0][2] | xg[NQT - 1][2]) != 0;
     }
     // blocks [blo, blo + nblk) hold the live KV positions of the workgroup's
     // rows (all of them without a mask, or with mslow);
@@ -333,177 +363,186 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         nblk = (int)((hi + BK - 1) / BK) - blo;
         ni = (nblk + KVG - 1) / KVG;
     }
-    const int bs = blo + min(kg * ni, nblk);
-    const int ng = min(ni, blo + nblk - bs);
+    // The rest of the kernel, in two copies under a mask tensor (MM = 1):
+    // workgroups whose rows are all intervals, and workgroups that add the
+    // mask per element (SLOW). With the per-element code inside the one
+    // pipelined loop the compiler lays out the interval path differently
+    // (fewer unrolled MFMA groups, twice the register moves), measured at
+    // 3.7 us more per realtime-encoder layer.
+    auto rest = [&](auto slow_tag) __attribute__((always_inline)) {
+        constexpr bool SLOW = decltype(slow_tag)::value;
+        static_assert(!SLOW || MM == 1, "the per-element path is the mask tensor's");
+        const int bs = blo + min(kg * ni, nblk);
+        const int ng = min(ni, blo + nblk - bs);
 
 
-    // ---- block loads: global -> LDS ring -------------------------------------
-    // Instruction i of wavefront wq fills rows [8 (NQT i + wq), + 8) of the
-    // group's block; lane l writes LDS chunk l % 8 of row + l / 8, which holds
-    // the row's chunk (l % 8) ^ swizzle(row). A block's rows start at a
-    // scalar base plus a 32-bit lane offset (row strides are below 8 MiB,
-    // checked by the host); the partial last block clamps rows past n_kv to
-    // row n_kv - 1.
-    uint32_t ldk[NLD], ldv[NLD];
+        // ---- block loads: global -> LDS ring -------------------------------------
+        // Instruction i of wavefront wq fills rows [8 (NQT i + wq), + 8) of the
+        // group's block; lane l writes LDS chunk l % 8 of row + l / 8, which holds
+        // the row's chunk (l % 8) ^ swizzle(row). A block's rows start at a
+        // scalar base plus a 32-bit lane offset (row strides are below 8 MiB,
+        // checked by the host); the partial last block clamps rows past n_kv to
+        // row n_kv - 1.
+        uint32_t ldk[NLD], ldv[NLD];
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int r = 8 * (NQT * i + wq) + (lane >> 3);
-        ldk[i] = (uint32_t)r * (uint32_t)a.k_nb1 + ((lane & 7) ^ swz_k<D>(r)) * 16;
-        ldv[i] = (uint32_t)r * (uint32_t)a.v_nb1 + ((lane & 7) ^ swz_v<D>(r)) * 16;
-    }
-    const uint32_t lds0 = lds_offset(smem) + kg * GRP;
-    auto issue = [&](int blk) {   // blk: index within the group, < ng
-        const int kv0 = (bs + blk) * BK;
-        const uint32_t kd = lds0 + (blk % NS) * SLOT, vd = kd + BLK;
-        const char* kst = kb + (int64_t)kv0 * a.k_nb1;
-        const char* vst = vb + (int64_t)kv0 * a.v_nb1;
-        if (kv0 + BK <= a.nkv) {
-#pragma unroll
-            for (int i = 0; i < NLD; ++i) {
-                const uint32_t r0b = 8 * (NQT * i + wq) * ROW;
-                dma16(kst, ldk[i], kd + r0b);
-                dma16(vst, ldv[i], vd + r0b);
-            }
-        } else {
-            // once per head: the offsets are recomputed here rather than held
-            // in registers across the loop (the empty asm keeps them here)
-            int ln = lane;
-            asm volatile("" : "+v"(ln));
-            const int rmax = a.nkv - 1 - kv0;   // last valid row of the block (kv0 < n_kv)
-#pragma unroll
-            for (int i = 0; i < NLD; ++i) {
-                const int r0 = 8 * (NQT * i + wq);
-                const int r = r0 + (ln >> 3);
-                const int rc = min(r, rmax);
-                dma16(kst, (uint32_t)rc * (uint32_t)a.k_nb1 + ((ln & 7) ^ swz_k<D>(r)) * 16, kd + r0 * ROW);
-                dma16(vst, (uint32_t)rc * (uint32_t)a.v_nb1 + ((ln & 7) ^ swz_v<D>(r)) * 16, vd + r0 * ROW);
-            }
+        for (int i = 0; i < NLD; ++i) {
+            const int r = 8 * (NQT * i + wq) + (lane >> 3);
+            ldk[i] = (uint32_t)r * (uint32_t)a.k_nb1 + ((lane & 7) ^ swz_k<D>(r)) * 16;
+            ldv[i] = (uint32_t)r * (uint32_t)a.v_nb1 + ((lane & 7) ^ swz_v<D>(r)) * 16;
         }
-    };
-    const int npre = min(ng, NS - 1);
-    for (int blk = 0; blk < npre; ++blk) issue(blk);
-
-    // ---- Q: wait for its loads only, round to f16 (ggml's Q conversion, sign
-    // of the scale folded in), stage in LDS ------------------------------------
-    // (the npre blocks' loads were issued after the Q loads and may remain)
-    wait_blocks<NLD>(npre);
-    {
-        char* qs = smem + RING;
-        const float sg = a.scale_log2 < 0.f ? -1.0f : 1.0f;
+        const uint32_t lds0 = lds_offset(smem) + kg * GRP;
+        auto issue = [&](int blk) {   // blk: index within the group, < ng
+            const int kv0 = (bs + blk) * BK;
+            const uint32_t kd = lds0 + (blk % NS) * SLOT, vd = kd + BLK;
+            const char* kst = kb + (int64_t)kv0 * a.k_nb1;
+            const char* vst = vb + (int64_t)kv0 * a.v_nb1;
+            if (kv0 + BK <= a.nkv) {
 #pragma unroll
-        for (int u = 0; u < QPT; ++u) {
-            const int i = tid + NT * u;
-            const int r = i / QCH, cch = i % QCH;
-            if (QF16) {
-                const half8 v = __builtin_bit_cast(half8, qraw[u]) * (_Float16)sg;
-                *(half8*)(qs + r * ROW + ((cch ^ (r & 7)) * 16)) = v;
+                for (int i = 0; i < NLD; ++i) {
+                    const uint32_t r0b = 8 * (NQT * i + wq) * ROW;
+                    dma16(kst, ldk[i], kd + r0b);
+                    dma16(vst, ldv[i], vd + r0b);
+                }
             } else {
-                half4 v;
+                // once per head: the offsets are recomputed here rather than held
+                // in registers across the loop (the empty asm keeps them here)
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const int rmax = a.nkv - 1 - kv0;   // last valid row of the block (kv0 < n_kv)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = (_Float16)(qraw[u][e] * sg);
-                *(half4*)(qs + r * ROW + (((cch >> 1) ^ (r & 7)) * 16) + (cch & 1) * 8) = v;
+                for (int i = 0; i < NLD; ++i) {
+                    const int r0 = 8 * (NQT * i + wq);
+                    const int r = r0 + (ln >> 3);
+                    const int rc = min(r, rmax);
+                    dma16(kst, (uint32_t)rc * (uint32_t)a.k_nb1 + ((ln & 7) ^ swz_k<D>(r)) * 16, kd + r0 * ROW);
+                    dma16(vst, (uint32_t)rc * (uint32_t)a.v_nb1 + ((ln & 7) ^ swz_v<D>(r)) * 16, vd + r0 * ROW);
+                }
+            }
+        };
+        const int npre = min(ng, NS - 1);
+        for (int blk = 0; blk < npre; ++blk) issue(blk);
+
+        // ---- Q: wait for its loads only, round to f16 (ggml's Q conversion, sign
+        // of the scale folded in), stage in LDS ------------------------------------
+        // (the npre blocks' loads were issued after the Q loads and may remain)
+        wait_blocks<NLD>(npre);
+        {
+            char* qs = smem + RING;
+            const float sg = a.scale_log2 < 0.f ? -1.0f : 1.0f;
+#pragma unroll
+            for (int u = 0; u < QPT; ++u) {
+                const int i = tid + NT * u;
+                const int r = i / QCH, cch = i % QCH;
+                const floatx4 qv = qw0 + r < a.nq ? qraw[u] : floatx4{0.f, 0.f, 0.f, 0.f};
+                if (QF16) {
+                    const half8 v = __builtin_bit_cast(half8, qv) * (_Float16)sg;
+                    *(half8*)(qs + r * ROW + ((cch ^ (r & 7)) * 16)) = v;
+                } else {
+                    half4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = (_Float16)(qv[e] * sg);
+                    *(half4*)(qs + r * ROW + (((cch >> 1) ^ (r & 7)) * 16) + (cch & 1) * 8) = v;
+                }
             }
         }
-    }
 
-    // ---- operand reads from LDS (offsets within a group's block) ----------------
-    // K: A-operand row nl of the 32-block is K row krow (the row-to-KV
-    // permutation), chunk 2 ks + hh.
-    int kaddr[KS];
-    {
-        const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
-        const int krow = ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
-        const int kx = hh ^ swz_k<D>(krow);
+        // ---- operand reads from LDS (offsets within a group's block) ----------------
+        // K: A-operand row nl of the 32-block is K row krow (the row-to-KV
+        // permutation), chunk 2 ks + hh.
+        int kaddr[KS];
+        {
+            const int am = nl >> 3, ahb = (nl >> 2) & 1, ab = nl & 3;
+            const int krow = ahb ? 16 + ((am + 2) & 3) * 4 + ab : 4 * am + ab;
+            const int kx = hh ^ swz_k<D>(krow);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kaddr[ks] = krow * ROW + ((2 * ks) ^ kx) * 16;
-    }
-    // V^T: operand (cc, db) covers the 8 positions of P operand cc, read as two
-    // transposed 8-byte loads 4 rows apart.
-    int vaddr[2][DB];
-    {
-        const int vq = (lane & 15) >> 2;
-        const int clo = 2 * ((lane & 31) >> 4) + ((lane & 3) >> 1);
+            for (int ks = 0; ks < KS; ++ks) kaddr[ks] = krow * ROW + ((2 * ks) ^ kx) * 16;
+        }
+        // V^T: operand (cc, db) covers the 8 positions of P operand cc, read as two
+        // transposed 8-byte loads 4 rows apart.
+        int vaddr[2][DB];
+        {
+            const int vq = (lane & 15) >> 2;
+            const int clo = 2 * ((lane & 31) >> 4) + ((lane & 3) >> 1);
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
+            for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
-                vaddr[cc][db] = ((hh ? 24 - 8 * cc : 8 * cc) + vq) * ROW + ((4 * db + clo) ^ swz_v<D>(vq)) * 16 +
-                                (lane & 1) * 8;
-    }
-    auto read_k = [&](int blk, half8 (&kr)[KS]) {
-        const char* base = smem + (blk % NS) * SLOT + kg * GRP;
+                for (int db = 0; db < DB; ++db)
+                    vaddr[cc][db] = ((hh ? 24 - 8 * cc : 8 * cc) + vq) * ROW + ((4 * db + clo) ^ swz_v<D>(vq)) * 16 +
+                                    (lane & 1) * 8;
+        }
+        auto read_k = [&](int blk, half8 (&kr)[KS]) {
+            const char* base = smem + (blk % NS) * SLOT + kg * GRP;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kr[ks] = *(const half8*)(base + kaddr[ks]);
-    };
-    auto read_v = [&](int blk, half8 (&vr)[2][DB]) {
-        const char* base = smem + (blk % NS) * SLOT + kg * GRP + BLK;
+            for (int ks = 0; ks < KS; ++ks) kr[ks] = *(const half8*)(base + kaddr[ks]);
+        };
+        auto read_v = [&](int blk, half8 (&vr)[2][DB]) {
+            const char* base = smem + (blk % NS) * SLOT + kg * GRP + BLK;
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
+            for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const half4 lo4 = lds_read_tr16(base + vaddr[cc][db]);
-                const half4 hi4 = lds_read_tr16(base + vaddr[cc][db] + 4 * ROW);
-                vr[cc][db] = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-            }
-    };
+                for (int db = 0; db < DB; ++db) {
+                    const half4 lo4 = lds_read_tr16(base + vaddr[cc][db]);
+                    const half4 hi4 = lds_read_tr16(base + vaddr[cc][db] + 4 * ROW);
+                    vr[cc][db] = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                }
+        };
 
-    // ---- MFMA groups and the softmax -------------------------------------------
-    auto s_mfma = [&](floatx16& s, const half8 (&q)[KS], const half8 (&kr)[KS]) {
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[0], q[0], floatx16{}, 0, 0, 0);
+        // ---- MFMA groups and the softmax -------------------------------------------
+        auto s_mfma = [&](floatx16& s, const half8 (&q)[KS], const half8 (&kr)[KS]) {
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[0], q[0], floatx16{}, 0, 0, 0);
 #pragma unroll
-        for (int ks = 1; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[ks], q[ks], s, 0, 0, 0);
-    };
-    auto pv_mfma = [&](floatx16 (&o)[DB], const half8 (&p)[2], const half8 (&vr)[2][DB]) {
+            for (int ks = 1; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[ks], q[ks], s, 0, 0, 0);
+        };
+        auto pv_mfma = [&](floatx16 (&o)[DB], const half8 (&p)[2], const half8 (&vr)[2][DB]) {
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
+            for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-            for (int db = 0; db < DB; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[cc][db], p[cc], o[db], 0, 0, 0);
-    };
-    // positions of the partial block blk at or past n_kv score -inf
-    auto tail_fix = [&](floatx16& sc, int blk) {
-        const int kv0 = (bs + blk) * BK;
+                for (int db = 0; db < DB; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[cc][db], p[cc], o[db], 0, 0, 0);
+        };
+        // positions of the partial block blk at or past n_kv score -inf
+        auto tail_fix = [&](floatx16& sc, int blk) {
+            const int kv0 = (bs + blk) * BK;
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-            if (kv0 + pf_kv_of(hh, j) >= a.nkv) sc[j] = -INFINITY;
-    };
-    // MM = 1 / 2: the live positions [rlo, rhi] of the lane's row in each
-    // half (clamped to [-1, n_kv]), and per half the largest lower bound and
-    // the smallest upper bound over its 32 rows (a block inside both is
-    // wholly live for the half)
-    int rlo[2] = {0, 0}, rhi[2] = {0, 0}, hlo[2] = {0, 0}, hhi[2] = {0, 0};
-    if constexpr (MM == 1) {
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            rlo[x] = ivl[x].x;
-            rhi[x] = ivl[x].y;
-            // (lanes l and l + 32 hold the same row; uniform results)
-            hlo[x] = __builtin_amdgcn_readfirstlane(wave_max_i(rlo[x]));
-            hhi[x] = __builtin_amdgcn_readfirstlane(wave_min_i(rhi[x]));
-        }
-    }
-    if constexpr (MM == 2) {
-        auto clampkv = [&](int64_t x) { return (int)(x < -1 ? -1 : (x > a.nkv ? a.nkv : x)); };
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            const int64_t r0 = (int64_t)qw0 + 64 * wq + 32 * x;
-            const int64_t wb = a.im_window > 0 ? a.im_offset - a.im_window + 1 : INT64_MIN / 2;
-            rlo[x] = clampkv(r0 + nl + wb);
-            rhi[x] = clampkv(r0 + nl + a.im_offset);
-            hlo[x] = clampkv(r0 + 31 + wb);
-            hhi[x] = clampkv(r0 + a.im_offset);
-        }
-    }
-    // MM = 1 / 2: block blk (of this group) for half x; a uniform branch,
-    // taken only for blocks not wholly live for the half's rows. MM = 1,
-    // mslow: every score gets its mask value (per element loads; -inf, and
-    // a position past n_kv, remove it; a finite value m adds m / |scale|,
-    // so that c s becomes c s + m log2(e)). The lane's mask row (rows past
-    // n_q read row n_q - 1; their outputs are not stored) is addressed here
-    // rather than held in registers across the loop (the empty asm keeps
-    // the computation here).
-    auto mask_fix = [&](floatx16& sc, int blk, int x) {
+            for (int j = 0; j < 16; ++j)
+                if (kv0 + pf_kv_of(hh, j) >= a.nkv) sc[j] = -INFINITY;
+        };
+        // MM = 1 / 2: the live positions [rlo, rhi] of the lane's row in each
+        // half (clamped to [-1, n_kv]), and per half the largest lower bound and
+        // the smallest upper bound over its 32 rows (a block inside both is
+        // wholly live for the half)
+        int rlo[2] = {0, 0}, rhi[2] = {0, 0}, hlo[2] = {0, 0}, hhi[2] = {0, 0};
         if constexpr (MM == 1) {
-            if (mslow) {
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                rlo[x] = ivl[x].x;
+                rhi[x] = ivl[x].y;
+                // (lanes l and l + 32 hold the same row; uniform results)
+                hlo[x] = __builtin_amdgcn_readfirstlane(wave_max_i(rlo[x]));
+                hhi[x] = __builtin_amdgcn_readfirstlane(wave_min_i(rhi[x]));
+            }
+        }
+        if constexpr (MM == 2) {
+            auto clampkv = [&](int64_t x) { return (int)(x < -1 ? -1 : (x > a.nkv ? a.nkv : x)); };
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                const int64_t r0 = (int64_t)qw0 + 64 * wq + 32 * x;
+                const int64_t wb = a.im_window > 0 ? a.im_offset - a.im_window + 1 : INT64_MIN / 2;
+                rlo[x] = clampkv(r0 + nl + wb);
+                rhi[x] = clampkv(r0 + nl + a.im_offset);
+                hlo[x] = clampkv(r0 + 31 + wb);
+                hhi[x] = clampkv(r0 + a.im_offset);
+            }
+        }
+        // MM = 1 / 2: block blk (of this group) for half x; a uniform branch,
+        // taken only for blocks not wholly live for the half's rows. SLOW:
+        // every score gets its mask value (per element loads; -inf, and
+        // a position past n_kv, remove it; a finite value m adds m / |scale|,
+        // so that c s becomes c s + m log2(e)). The lane's mask row (rows past
+        // n_q read row n_q - 1; their outputs are not stored) is addressed here
+        // rather than held in registers across the loop (the empty asm keeps
+        // the computation here).
+        auto mask_fix = [&](floatx16& sc, int blk, int x) {
+            if constexpr (SLOW) {
                 int ln = lane;
                 asm volatile("" : "+v"(ln));
                 const int row = min(qw0 + 64 * wq + 32 * x + (ln & 31), a.nq - 1);
@@ -519,313 +558,317 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
                     sc[j] = (mv[j] == kF16NegInf || kv0 + pf_kv_of(ln >> 5, j) >= a.nkv)
                                 ? -INFINITY
                                 : fmaf(f16_bits_to_f32(mv[j]), inv_sc, sc[j]);
-                return;
-            }
-        }
-        if constexpr (MM != 0) {
-            const int kv0 = (bs + blk) * BK;
-            if (!(kv0 >= hlo[x] && kv0 + BK - 1 <= hhi[x])) {
+            } else if constexpr (MM != 0) {
+                const int kv0 = (bs + blk) * BK;
+                if (!(kv0 >= hlo[x] && kv0 + BK - 1 <= hhi[x])) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int kv = kv0 + pf_kv_of(hh, j);
-                    sc[j] = (kv < rlo[x] || kv > rhi[x]) ? -INFINITY : sc[j];
+                    for (int j = 0; j < 16; ++j) {
+                        const int kv = kv0 + pf_kv_of(hh, j);
+                        sc[j] = (kv < rlo[x] || kv > rhi[x]) ? -INFINITY : sc[j];
+                    }
                 }
             }
-        }
-    };
-    // P = 2^(c s - m) for the lane's 16 scores, as two f16 B operands, and
-    // their sum. With C8 (scale exactly 1/8) c is a literal and x = c s - m
-    // compiles to v_fmamk_f32, which issues at twice the rate of the
-    // three-register v_fma_f32; -m has to reach it as a plain register (a
-    // negation folded into the FMA would force the three-register form), so
-    // it passes through an empty asm. (Every instruction that reads an MFMA
-    // result must be one the compiler sees: it alone inserts the wait states
-    // such a read needs.)
-    const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-    auto exps = [&](const floatx16& sc, float m, half8 (&p)[2]) -> float {
-        float nm = (m == -INFINITY) ? 0.f : -m;
-        asm("" : "+v"(nm));
-        float ls[2] = {0.f, 0.f};
+        };
+        // P = 2^(c s - m) for the lane's 16 scores, as two f16 B operands, and
+        // their sum. With C8 (scale exactly 1/8) c is a literal and x = c s - m
+        // compiles to v_fmamk_f32, which issues at twice the rate of the
+        // three-register v_fma_f32; -m has to reach it as a plain register (a
+        // negation folded into the FMA would force the three-register form), so
+        // it passes through an empty asm. (Every instruction that reads an MFMA
+        // result must be one the compiler sees: it alone inserts the wait states
+        // such a read needs.)
+        const half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+        auto exps = [&](const floatx16& sc, float m, half8 (&p)[2]) -> float {
+            float nm = (m == -INFINITY) ? 0.f : -m;
+            asm("" : "+v"(nm));
+            float ls[2] = {0.f, 0.f};
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
+            for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                p[cc][i] = (_Float16)exp2_fast(fmaf(sc[8 * cc + i], C8 ? 0.18033688f : c, nm));
+                for (int i = 0; i < 8; ++i)
+                    p[cc][i] = (_Float16)exp2_fast(fmaf(sc[8 * cc + i], C8 ? 0.18033688f : c, nm));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const half2 p2 = {p[cc][2 * i], p[cc][2 * i + 1]};
-                ls[i & 1] = __builtin_amdgcn_fdot2(p2, ones, ls[i & 1], false);
+                for (int i = 0; i < 4; ++i) {
+                    const half2 p2 = {p[cc][2 * i], p[cc][2 * i + 1]};
+                    ls[i & 1] = __builtin_amdgcn_fdot2(p2, ones, ls[i & 1], false);
+                }
+            }
+            return ls[0] + ls[1];
+        };
+        // the block's max (log2 units) over the lane pair
+        auto block_max = [&](const floatx16& sc) -> float {
+            float r = sc[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) r = fmaxf(r, sc[j]);
+            return pair32_max(r) * c;
+        };
+        // raise the running max to mx: rescale O and l
+        auto raise = [&](float mx, float& m, float& l, floatx16 (&o)[DB]) {
+            const float mnew = fmaxf(m, mx);
+            const float ms = (mnew == -INFINITY) ? 0.f : mnew;
+            const float alpha = exp2_fast(m - ms);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
+            l *= alpha;
+            m = mnew;
+        };
+        // With a mask, rows past n_q (their outputs are not stored) take no part
+        // in the wavefront's choice of the exact path: its rows then see the same
+        // choices under any two masks that agree on the real rows (an implicit
+        // mask and the same mask as a tensor give the same bits). Such a row may
+        // keep m = -inf and turn its own P, l and O to inf / NaN; each row's
+        // values stay in its own column of P and O and are dropped at the store.
+        const bool real_a = MM == 0 || qw0 + 64 * wq + nl < a.nq;
+        const bool real_b = MM == 0 || qw0 + 64 * wq + 32 + nl < a.nq;
+        // softmax of one block, max first (blocks outside the pipelined loop)
+        auto softmax_exact = [&](const floatx16& sc, float& m, float& l, floatx16 (&o)[DB], half8 (&p)[2], bool real) {
+            const float mx = block_max(sc);
+            if (__any(mx > m + TAU && real)) raise(mx, m, l, o);
+            l += exps(sc, m, p);
+        };
+        // Softmax inside the pipelined loop. P is computed against the current
+        // running max m with no block max at all: a score more than TAU above m
+        // makes some P > 2^TAU, so the lane's sum of its 16 P exceeds 2^TAU (and is
+        // inf or NaN past the f16 range). Only then (rare once m has settled) is
+        // the block max reduced, O and l rescaled and P recomputed; a large sum of
+        // moderate P can also take that path, which is harmless. Once m is raised
+        // every P of later blocks stays below 2^TAU unless a new larger score
+        // arrives, which the same test catches.
+        // The basic block of each half (closed by that branch) holds its 8 MFMAs
+        // and the softmax's fast path; HALF (1 or 2) lays them out: in H1 the 4
+        // K operand reads first, then softmax VALU work while they land, then one
+        // MFMA per 5 VALU instructions; in H2 (operands in registers) one MFMA per
+        // 6 from the start.
+        auto softmax_spec = [&](auto half_tag, const floatx16& sc, float& m, float& l, floatx16 (&o)[DB],
+                                half8 (&p)[2], bool real) {
+            constexpr int HALF = decltype(half_tag)::value;
+            float ls = exps(sc, m, p);
+            if constexpr (HALF == 1) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS reads
+                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);   // VALU
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // VALU
+                }
+            } else if constexpr (HALF == 2) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
+            }
+            // 2^TAU (also true for inf / NaN); with a mask, also a row that has
+            // no live score yet (its P above were taken against m = 0)
+            bool slow = !(ls <= 256.0f);
+            if constexpr (MM != 0) slow = (slow || m == -INFINITY) && real;
+            if (__any(slow)) {
+                raise(block_max(sc), m, l, o);
+                ls = exps(sc, m, p);
+            }
+            l += ls;
+        };
+
+        floatx16 oa[DB], ob[DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db) { oa[db] = floatx16{}; ob[db] = floatx16{}; }
+        float ma = -INFINITY, mb = -INFINITY, la = 0.f, lb = 0.f;
+        floatx16 sa, sb;
+        half8 pa[2], pb[2];
+        half8 kr[KS];
+        half8 vr[2][DB];
+
+        // Full blocks of this group run through the pipelined loop; the partial
+        // last block of the KV range (only the last group can hold it) is computed
+        // on its own after them, so the loop body needs no position checks.
+        const bool part = ng > 0 && (bs + ng) * BK > a.nkv;
+        const int nf = ng - (part ? 1 : 0);
+
+        // ---- prologue: blocks 0 and 1 landed; Q operands; S_A(0), S_B(0), P_A(0) ----
+        wait_blocks<NLD>(max(npre - 2, 0));
+        __syncthreads();   // Q staged, blocks 0 and 1 visible
+        half8 qa[KS], qb[KS];
+        {
+            const char* qs = smem + RING;
+            const int ra = 64 * wq + nl, rb = ra + 32;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                qa[ks] = *(const half8*)(qs + ra * ROW + (((2 * ks + hh) ^ (ra & 7)) * 16));
+                qb[ks] = *(const half8*)(qs + rb * ROW + (((2 * ks + hh) ^ (rb & 7)) * 16));
             }
         }
-        return ls[0] + ls[1];
-    };
-    // the block's max (log2 units) over the lane pair
-    auto block_max = [&](const floatx16& sc) -> float {
-        float r = sc[0];
+        if (nf > 0) {
+            read_k(0, kr);
+            read_v(0, vr);
+            s_mfma(sa, qa, kr);
+            s_mfma(sb, qb, kr);
+            mask_fix(sa, 0, 0);
+            mask_fix(sb, 0, 1);
+            softmax_exact(sa, ma, la, oa, pa, real_a);
+            // the loop's softmax needs a finite running max to start from
+            mb = block_max(sb);
+        }
+
+        // ---- main loop: full blocks 0 .. nf - 2 ------------------------------------
+        // Copies: blocks 0 .. NS - 2 before the loop; between the halves of
+        // iteration 0 block NS - 1 (its slot is still unused), of iteration
+        // t >= 1 block t + NS into the slot of block t (read in iteration t - 1,
+        // before its barrier); block NS at the top of iteration 1 (block 0 is
+        // read after the prologue's barrier). At the end of iteration t block
+        // t + 2 must have landed (read at the top of iteration t + 1). Every
+        // wavefront passes one barrier per block of the longest group (ni), plus
+        // the prologue's and the merge's.
+        for (int t = 0; t + 1 < nf; ++t) {
+            if (t == 1 && NS < ng) issue(NS);
+            read_k(t + 1, kr);
+            if (t > 0) mask_fix(sb, t, 1);   // S_B(t), from H2 of the previous iteration
+            // H1: PV_A(t), S_A(t+1) on the matrix pipe; softmax of S_B(t). The
+            // MFMAs come first in the source so they share a basic block with
+            // the softmax's fast path (its rare rescale branch closes the block)
+            // and the scheduler can interleave the two; PV_A first, as its
+            // operands are in registers while K_{t+1} lands.
+            pv_mfma(oa, pa, vr);
+            s_mfma(sa, qa, kr);
+            softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb, real_b);
+            if ((t == 0 ? NS - 1 : t + NS) < ng) issue(t == 0 ? NS - 1 : t + NS);
+            // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
+            mask_fix(sa, t + 1, 0);
+            pv_mfma(ob, pb, vr);
+            read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
+            s_mfma(sb, qb, kr);
+            softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa, real_a);
+            // blocks issued so far: up to NS - 1 (t = 0), t + NS (t >= 1)
+            const int last = min(t >= 1 ? t + NS : NS - 1, ng - 1);
+            wait_blocks_loop<NLD>(last - (t + 2));   // 2 at most: last <= t + NS
+            __syncthreads();
+        }
+        // (no loads are issued from here on)
+        if (nf > 0) {
+            // last full block: PV_A, softmax of S_B, PV_B
+            if (nf > 1) mask_fix(sb, nf - 1, 1);
+            pv_mfma(oa, pa, vr);
+            softmax_exact(sb, mb, lb, ob, pb, real_b);
+            pv_mfma(ob, pb, vr);
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
+        if (part) {
+            // the partial block, unpipelined
+            const int tp = nf;
+            read_k(tp, kr);
+            s_mfma(sa, qa, kr);
+            s_mfma(sb, qb, kr);
+            read_v(tp, vr);
+            tail_fix(sa, tp);
+            tail_fix(sb, tp);
+            mask_fix(sa, tp, 0);
+            mask_fix(sb, tp, 1);
+            softmax_exact(sa, ma, la, oa, pa, real_a);
+            softmax_exact(sb, mb, lb, ob, pb, real_b);
+            pv_mfma(oa, pa, vr);
+            pv_mfma(ob, pb, vr);
+            __syncthreads();
+        }
+        for (int tt = ng; tt < ni; ++tt) __syncthreads();
+
+        // ---- merge the KV groups through LDS (the ring is free), normalise ------------
+        // Every wavefront publishes its (O, m, l) as 17 chunks of 4 floats per lane,
+        // chunk-major (chunk c of lane l at floats 256 c + 4 l: one 16-byte write
+        // and read per chunk, the 64 lanes' chunks contiguous): chunk c < 16 holds
+        // O elements 4c .. 4c + 3 (element e = 32 x + 16 v + j is accumulator j of
+        // vector v of half x), chunk 16 holds (m_A, m_B, l_A, l_B). Wavefront
+        // (kg, wq) then merges elements [16 kg, 16 kg + 16) of query tile wq over
+        // all groups (one O vector of one half), in group order, and after a
+        // barrier (the staging tile overlaps the published data) writes them
+        // normalised to the staging tile, row r at r * 256 bytes with 16-byte
+        // chunk j at position j ^ (r & 15); then all wavefronts store full rows.
+        constexpr int EPW = 64 / KVG;                   // elements merged per wavefront
+        static_assert(EPW % 4 == 0 && EPW <= 32, "a wavefront's elements lie in one half");
+        static_assert(PUB == 17 * 4, "published chunks");
+        float* xs = (float*)smem;
+        char* ost = smem;
+        {
+            floatx4* w = (floatx4*)(xs + (kg * NQT + wq) * PUB * 64) + lane;
 #pragma unroll
-        for (int j = 1; j < 16; ++j) r = fmaxf(r, sc[j]);
-        return pair32_max(r) * c;
-    };
-    // raise the running max to mx: rescale O and l
-    auto raise = [&](float mx, float& m, float& l, floatx16 (&o)[DB]) {
-        const float mnew = fmaxf(m, mx);
-        const float ms = (mnew == -INFINITY) ? 0.f : mnew;
-        const float alpha = exp2_fast(m - ms);
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
-        l *= alpha;
-        m = mnew;
-    };
-    // With a mask, rows past n_q (their outputs are not stored) take no part
-    // in the wavefront's choice of the exact path: its rows then see the same
-    // choices under any two masks that agree on the real rows (an implicit
-    // mask and the same mask as a tensor give the same bits). Such a row may
-    // keep m = -inf and turn its own P, l and O to inf / NaN; each row's
-    // values stay in its own column of P and O and are dropped at the store.
-    const bool real_a = MM == 0 || qw0 + 64 * wq + nl < a.nq;
-    const bool real_b = MM == 0 || qw0 + 64 * wq + 32 + nl < a.nq;
-    // softmax of one block, max first (blocks outside the pipelined loop)
-    auto softmax_exact = [&](const floatx16& sc, float& m, float& l, floatx16 (&o)[DB], half8 (&p)[2], bool real) {
-        const float mx = block_max(sc);
-        if (__any(mx > m + TAU && real)) raise(mx, m, l, o);
-        l += exps(sc, m, p);
-    };
-    // Softmax inside the pipelined loop. P is computed against the current
-    // running max m with no block max at all: a score more than TAU above m
-    // makes some P > 2^TAU, so the lane's sum of its 16 P exceeds 2^TAU (and is
-    // inf or NaN past the f16 range). Only then (rare once m has settled) is
-    // the block max reduced, O and l rescaled and P recomputed; a large sum of
-    // moderate P can also take that path, which is harmless. Once m is raised
-    // every P of later blocks stays below 2^TAU unless a new larger score
-    // arrives, which the same test catches.
-    // The basic block of each half (closed by that branch) holds its 8 MFMAs
-    // and the softmax's fast path; HALF (1 or 2) lays them out: in H1 the 4
-    // K operand reads first, then softmax VALU work while they land, then one
-    // MFMA per 5 VALU instructions; in H2 (operands in registers) one MFMA per
-    // 6 from the start.
-    auto softmax_spec = [&](auto half_tag, const floatx16& sc, float& m, float& l, floatx16 (&o)[DB],
-                            half8 (&p)[2], bool real) {
-        constexpr int HALF = decltype(half_tag)::value;
-        float ls = exps(sc, m, p);
-        if constexpr (HALF == 1) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS reads
-            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);   // VALU
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // VALU
+            for (int ci = 0; ci < 16; ++ci) {
+                const floatx16& o = (ci < 8) ? oa[(ci % 8) / 4] : ob[(ci % 8) / 4];
+                const int j0 = 4 * (ci % 4);
+                w[ci * 64] = floatx4{o[j0], o[j0 + 1], o[j0 + 2], o[j0 + 3]};
             }
-        } else if constexpr (HALF == 2) {
+            w[16 * 64] = floatx4{ma, mb, la, lb};
+        }
+        __syncthreads();
+        const int e0 = kg * EPW;        // first element: 0..31 half A, 32..63 half B
+        const int x = e0 / 32;
+        floatx4 res[EPW / 4];
+        {
+            float mg[KVG], lg[KVG];
+            float M = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            for (int g = 0; g < KVG; ++g) {
+                const floatx4 ml = ((const floatx4*)(xs + (g * NQT + wq) * PUB * 64))[16 * 64 + lane];
+                mg[g] = x ? ml[1] : ml[0];
+                lg[g] = x ? ml[3] : ml[2];
+                M = fmaxf(M, mg[g]);
             }
-        }
-        // 2^TAU (also true for inf / NaN); with a mask, also a row that has
-        // no live score yet (its P above were taken against m = 0)
-        bool slow = !(ls <= 256.0f);
-        if constexpr (MM != 0) slow = (slow || m == -INFINITY) && real;
-        if (__any(slow)) {
-            raise(block_max(sc), m, l, o);
-            ls = exps(sc, m, p);
-        }
-        l += ls;
-    };
-
-    floatx16 oa[DB], ob[DB];
+            const float Ms = (M == -INFINITY) ? 0.f : M;
+            float wg[KVG];
+            float lsum = 0.f;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) { oa[db] = floatx16{}; ob[db] = floatx16{}; }
-    float ma = -INFINITY, mb = -INFINITY, la = 0.f, lb = 0.f;
-    floatx16 sa, sb;
-    half8 pa[2], pb[2];
-    half8 kr[KS];
-    half8 vr[2][DB];
-
-    // Full blocks of this group run through the pipelined loop; the partial
-    // last block of the KV range (only the last group can hold it) is computed
-    // on its own after them, so the loop body needs no position checks.
-    const bool part = ng > 0 && (bs + ng) * BK > a.nkv;
-    const int nf = ng - (part ? 1 : 0);
-
-    // ---- prologue: blocks 0 and 1 landed; Q operands; S_A(0), S_B(0), P_A(0) ----
-    wait_blocks<NLD>(max(npre - 2, 0));
-    __syncthreads();   // Q staged, blocks 0 and 1 visible
-    half8 qa[KS], qb[KS];
-    {
-        const char* qs = smem + RING;
-        const int ra = 64 * wq + nl, rb = ra + 32;
+            for (int g = 0; g < KVG; ++g) {
+                wg[g] = exp2_fast(mg[g] - Ms);
+                lsum = fmaf(wg[g], lg[g], lsum);
+            }
+            const float lt = pair32_sum(lsum);
+            const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            qa[ks] = *(const half8*)(qs + ra * ROW + (((2 * ks + hh) ^ (ra & 7)) * 16));
-            qb[ks] = *(const half8*)(qs + rb * ROW + (((2 * ks + hh) ^ (rb & 7)) * 16));
-        }
-    }
-    if (nf > 0) {
-        read_k(0, kr);
-        read_v(0, vr);
-        s_mfma(sa, qa, kr);
-        s_mfma(sb, qb, kr);
-        mask_fix(sa, 0, 0);
-        mask_fix(sb, 0, 1);
-        softmax_exact(sa, ma, la, oa, pa, real_a);
-        // the loop's softmax needs a finite running max to start from
-        mb = block_max(sb);
-    }
-
-    // ---- main loop: full blocks 0 .. nf - 2 ------------------------------------
-    // Copies: blocks 0 .. NS - 2 before the loop; between the halves of
-    // iteration 0 block NS - 1 (its slot is still unused), of iteration
-    // t >= 1 block t + NS into the slot of block t (read in iteration t - 1,
-    // before its barrier); block NS at the top of iteration 1 (block 0 is
-    // read after the prologue's barrier). At the end of iteration t block
-    // t + 2 must have landed (read at the top of iteration t + 1). Every
-    // wavefront passes one barrier per block of the longest group (ni), plus
-    // the prologue's and the merge's.
-    for (int t = 0; t + 1 < nf; ++t) {
-        if (t == 1 && NS < ng) issue(NS);
-        read_k(t + 1, kr);
-        if (t > 0) mask_fix(sb, t, 1);   // S_B(t), from H2 of the previous iteration
-        // H1: PV_A(t), S_A(t+1) on the matrix pipe; softmax of S_B(t). The
-        // MFMAs come first in the source so they share a basic block with
-        // the softmax's fast path (its rare rescale branch closes the block)
-        // and the scheduler can interleave the two; PV_A first, as its
-        // operands are in registers while K_{t+1} lands.
-        pv_mfma(oa, pa, vr);
-        s_mfma(sa, qa, kr);
-        softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb, real_b);
-        if ((t == 0 ? NS - 1 : t + NS) < ng) issue(t == 0 ? NS - 1 : t + NS);
-        // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
-        mask_fix(sa, t + 1, 0);
-        pv_mfma(ob, pb, vr);
-        read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
-        s_mfma(sb, qb, kr);
-        softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa, real_a);
-        // blocks issued so far: up to NS - 1 (t = 0), t + NS (t >= 1)
-        const int last = min(t >= 1 ? t + NS : NS - 1, ng - 1);
-        wait_blocks_loop<NLD>(last - (t + 2));   // 2 at most: last <= t + NS
-        __syncthreads();
-    }
-    // (no loads are issued from here on)
-    if (nf > 0) {
-        // last full block: PV_A, softmax of S_B, PV_B
-        if (nf > 1) mask_fix(sb, nf - 1, 1);
-        pv_mfma(oa, pa, vr);
-        softmax_exact(sb, mb, lb, ob, pb, real_b);
-        pv_mfma(ob, pb, vr);
-        wait_vmcnt<0>();
-        __syncthreads();
-    }
-    if (part) {
-        // the partial block, unpipelined
-        const int tp = nf;
-        read_k(tp, kr);
-        s_mfma(sa, qa, kr);
-        s_mfma(sb, qb, kr);
-        read_v(tp, vr);
-        tail_fix(sa, tp);
-        tail_fix(sb, tp);
-        mask_fix(sa, tp, 0);
-        mask_fix(sb, tp, 1);
-        softmax_exact(sa, ma, la, oa, pa, real_a);
-        softmax_exact(sb, mb, lb, ob, pb, real_b);
-        pv_mfma(oa, pa, vr);
-        pv_mfma(ob, pb, vr);
-        __syncthreads();
-    }
-    for (int tt = ng; tt < ni; ++tt) __syncthreads();
-
-    // ---- merge the KV groups through LDS (the ring is free), normalise ------------
-    // Every wavefront publishes its (O, m, l) as 17 chunks of 4 floats per lane,
-    // chunk-major (chunk c of lane l at floats 256 c + 4 l: one 16-byte write
-    // and read per chunk, the 64 lanes' chunks contiguous): chunk c < 16 holds
-    // O elements 4c .. 4c + 3 (element e = 32 x + 16 v + j is accumulator j of
-    // vector v of half x), chunk 16 holds (m_A, m_B, l_A, l_B). Wavefront
-    // (kg, wq) then merges elements [16 kg, 16 kg + 16) of query tile wq over
-    // all groups (one O vector of one half), in group order, and after a
-    // barrier (the staging tile overlaps the published data) writes them
-    // normalised to the staging tile, row r at r * 256 bytes with 16-byte
-    // chunk j at position j ^ (r & 15); then all wavefronts store full rows.
-    constexpr int EPW = 64 / KVG;                   // elements merged per wavefront
-    static_assert(EPW % 4 == 0 && EPW <= 32, "a wavefront's elements lie in one half");
-    static_assert(PUB == 17 * 4, "published chunks");
-    float* xs = (float*)smem;
-    char* ost = smem;
-    {
-        floatx4* w = (floatx4*)(xs + (kg * NQT + wq) * PUB * 64) + lane;
+            for (int g = 0; g < KVG; ++g) wg[g] *= inv;
+            floatx4 og[KVG][EPW / 4];
 #pragma unroll
-        for (int ci = 0; ci < 16; ++ci) {
-            const floatx16& o = (ci < 8) ? oa[(ci % 8) / 4] : ob[(ci % 8) / 4];
-            const int j0 = 4 * (ci % 4);
-            w[ci * 64] = floatx4{o[j0], o[j0 + 1], o[j0 + 2], o[j0 + 3]};
-        }
-        w[16 * 64] = floatx4{ma, mb, la, lb};
-    }
-    __syncthreads();
-    const int e0 = kg * EPW;        // first element: 0..31 half A, 32..63 half B
-    const int x = e0 / 32;
-    floatx4 res[EPW / 4];
-    {
-        float mg[KVG], lg[KVG];
-        float M = -INFINITY;
+            for (int g = 0; g < KVG; ++g)
 #pragma unroll
-        for (int g = 0; g < KVG; ++g) {
-            const floatx4 ml = ((const floatx4*)(xs + (g * NQT + wq) * PUB * 64))[16 * 64 + lane];
-            mg[g] = x ? ml[1] : ml[0];
-            lg[g] = x ? ml[3] : ml[2];
-            M = fmaxf(M, mg[g]);
-        }
-        const float Ms = (M == -INFINITY) ? 0.f : M;
-        float wg[KVG];
-        float lsum = 0.f;
-#pragma unroll
-        for (int g = 0; g < KVG; ++g) {
-            wg[g] = exp2_fast(mg[g] - Ms);
-            lsum = fmaf(wg[g], lg[g], lsum);
-        }
-        const float lt = pair32_sum(lsum);
-        const float inv = (lt == 0.f) ? 0.f : 1.0f / lt;
-#pragma unroll
-        for (int g = 0; g < KVG; ++g) wg[g] *= inv;
-        floatx4 og[KVG][EPW / 4];
-#pragma unroll
-        for (int g = 0; g < KVG; ++g)
+                for (int q = 0; q < EPW / 4; ++q)
+                    og[g][q] = ((const floatx4*)(xs + (g * NQT + wq) * PUB * 64))[(e0 / 4 + q) * 64 + lane];
 #pragma unroll
             for (int q = 0; q < EPW / 4; ++q)
-                og[g][q] = ((const floatx4*)(xs + (g * NQT + wq) * PUB * 64))[(e0 / 4 + q) * 64 + lane];
 #pragma unroll
-        for (int q = 0; q < EPW / 4; ++q)
+                for (int e = 0; e < 4; ++e) {
+                    float acc = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float acc = 0.f;
+                    for (int g = 0; g < KVG; ++g) acc = fmaf(wg[g], og[g][q][e], acc);
+                    res[q][e] = acc;
+                }
+        }
+        __syncthreads();   // every read of the published data is done
+        {
+            const int row = 64 * wq + 32 * x + nl;
 #pragma unroll
-                for (int g = 0; g < KVG; ++g) acc = fmaf(wg[g], og[g][q][e], acc);
-                res[q][e] = acc;
+            for (int q = 0; q < EPW / 4; ++q) {
+                const int eh = e0 - 32 * x + 4 * q;              // element within the half: 16 db + 4 a4
+                const int ch = 8 * (eh / 16) + 2 * ((eh % 16) / 4) + hh;   // dims 4 ch .. 4 ch + 3
+                *(floatx4*)(ost + row * 256 + ((ch ^ (row & 15)) * 16)) = res[q];
             }
-    }
-    __syncthreads();   // every read of the published data is done
-    {
-        const int row = 64 * wq + 32 * x + nl;
-#pragma unroll
-        for (int q = 0; q < EPW / 4; ++q) {
-            const int eh = e0 - 32 * x + 4 * q;              // element within the half: 16 db + 4 a4
-            const int ch = 8 * (eh / 16) + 2 * ((eh % 16) / 4) + hh;   // dims 4 ch .. 4 ch + 3
-            *(floatx4*)(ost + row * 256 + ((ch ^ (row & 15)) * 16)) = res[q];
         }
-    }
-    __syncthreads();
-    // ---- store: dst[b][row][h][0..63], 16 threads per 256-byte row -------------
+        __syncthreads();
+        // ---- store: dst[b][row][h][0..63], 16 threads per 256-byte row -------------
 #pragma unroll
-    for (int u = 0; u < BM * 16 / NT; ++u) {
-        const int i = tid + NT * u;
-        const int r = i >> 4, ch = i & 15;
-        const int row = qw0 + r;
-        if (row < a.nq) {
-            const floatx4 v = *(const floatx4*)(ost + r * 256 + ((ch ^ (r & 15)) * 16));
-            __builtin_nontemporal_store(v, (floatx4*)(a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 4 * ch));
+        for (int u = 0; u < BM * 16 / NT; ++u) {
+            const int i = tid + NT * u;
+            const int r = i >> 4, ch = i & 15;
+            const int row = qw0 + r;
+            if (row < a.nq) {
+                const floatx4 v = *(const floatx4*)(ost + r * 256 + ((ch ^ (r & 15)) * 16));
+                __builtin_nontemporal_store(v, (floatx4*)(a.dst + (((int64_t)b * a.nq + row) * a.hq + h) * D + 4 * ch));
+            }
         }
+    };
+    if constexpr (MM == 1) {
+        if (mslow) rest(std::true_type{});
+        else rest(std::false_type{});
+    } else {
+        rest(std::false_type{});
     }
 }
 
@@ -859,7 +902,7 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
         if (!a.mask_rows) return hipErrorInvalidValue;
         const int64_t nrows = (int64_t)a.nq * a.hm * a.bm;
         if (nrows > 0x7fffffff - 3) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(mask_rows_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, a.mask, a.m_nb1,
+        hipLaunchKernelGGL(mask_rows_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(64), 0, st, a.mask, a.m_nb1,
                            a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows);
         launch_pp_mm<1>(a, gm, nblk, ni, is_c8, grid, block, st);
     } else if (a.im_causal) {
