@@ -221,3 +221,19 @@ def test_rope_restatement_closed_forms():
     assert np.allclose(n0, n1, rtol=1e-5)
     ts = cases._powf(10000.0, np.float32(-2.0) / np.float32(8))
     assert abs(float(ts) - 10000.0 ** (-0.25)) < 1e-7
+
+
+def test_ggml_binding_loads_and_declines_without_a_gpu():
+    """The ggml-side binding (tests/ggml_binding/binding.c, compiled as C by
+    the build) links against libvxfa.so and loads; its supports_op declines
+    a node with attention sinks before any device access."""
+    path = os.path.join(ROOT, "tests", "ggml_binding", "libvxfa_ggml_binding.so")
+    if not os.path.exists(path):
+        pytest.skip("the binding library is built by __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    f = lib.vxfa_test_decoder_node
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 8 + [ctypes.c_void_p] * 2 + [ctypes.c_int]
+    buf = (ctypes.c_float * 4096)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert f(None, None, p, p, p, 30, 8192, 0, 32, 8, 128, 1, 16, None, p, 1) == 0
