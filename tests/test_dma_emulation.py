@@ -72,3 +72,40 @@ def test_emulation_catches_planted_mistakes():
             pp_copy(sh, 2, 4, 4, 0, 0, 3, 0, Mem())   # block 3 = rows 96..127 of 100
     finally:
         dma_emul.np.minimum = orig
+
+
+# ---- the masked hd 128 prefill (fa_prefill.hip), shipped and reordered ----
+
+from prefill_emul import emulate_prefill_masked  # noqa: E402
+
+# decoder prefill 439 causal (the shape whose reordered variant faulted),
+# prefills after cached rows, a single row group, n_kv past one step, a
+# sliding window (workgroups whose live range starts past step 0) and rows
+# with no live position
+PREFILL_CASES = [
+    dict(nq=439, nkv=439), dict(nq=100, nkv=439), dict(nq=64, nkv=8192), dict(nq=1, nkv=129),
+    dict(nq=300, nkv=1000, mask_fn=lambda i, j: i + 700 - 200 < j <= i + 700),
+    dict(nq=130, nkv=300, mask_fn=lambda i, j: i < 64 and j <= i),
+]
+
+
+@pytest.mark.parametrize("order", ["shipped", "copies_first"])
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=lambda c: f"nq{c['nq']}_nkv{c['nkv']}")
+def test_masked_prefill_schedule(case, order):
+    """Copies in bounds, no LDS access racing a copy in flight, every step's
+    copies landed before its reads, no wavefront ending with a copy in
+    flight: for the shipped order and for step 0's copies issued before the
+    mask scan."""
+    emulate_prefill_masked(order=order, **case)
+
+
+@pytest.mark.parametrize("plant", ["issue_after_wait", "same_stage", "prefetch_at_end", "past_nkv"])
+def test_masked_prefill_emulation_catches_planted_mistakes(plant):
+    """A copy issued after the wait meant to cover it, a next step copied into
+    the stage being read, a copy still in flight when the wavefront ends, a
+    step past n_kv: each is reported."""
+    with pytest.raises(Violation):
+        emulate_prefill_masked(439, 439, order="shipped", plant=plant)
+    if plant != "issue_after_wait":   # the reordered form issues step 0 before every wait
+        with pytest.raises(Violation):
+            emulate_prefill_masked(439, 439, order="copies_first", plant=plant)
