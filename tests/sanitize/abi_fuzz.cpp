@@ -17,15 +17,12 @@
 namespace vxfa {
 hipError_t launch_decode(const AttnArgs&, int, int, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_prefill(const AttnArgs&, int, int, hipStream_t) { return hipErrorInvalidValue; }
-hipError_t launch_prefill64_pp(const AttnArgs&, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_prefill64_pp(const AttnArgs&, const StageReq*, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_prefill_pair(const AttnArgs&, hipStream_t) { return hipErrorInvalidValue; }
 bool prefill_pair_fits(const AttnArgs&) { return true; }
 hipError_t launch_zero(float*, int64_t, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_kv_append(const AppendArgs&, hipStream_t) { return hipErrorInvalidValue; }
-hipError_t launch_to_f16_kv(const float*, int64_t, int64_t, int64_t, const float*, int64_t, int64_t, int64_t, int, int,
-                            int, int, _Float16*, _Float16*, hipStream_t) {
-    return hipErrorInvalidValue;
-}
+hipError_t launch_to_f16_kv(const StageReq&, hipStream_t) { return hipErrorInvalidValue; }
 }  // namespace vxfa
 
 static int64_t pick(std::mt19937_64& g, const int64_t* v, int n) { return v[g() % n]; }

@@ -95,6 +95,20 @@ static void common(const AttnArgs& a) {
     if (!a.q || !a.k || !a.v || !a.dst) fail("null operand");
     if (a.hq % a.hkv || a.b % a.bk) fail("broadcast");
 }
+static void check_stage(const StageReq& r) {
+    const size_t bytes = (size_t)r.d * r.n * r.h * r.b * 2;
+    if (!r.k || !r.v) fail("staging source");
+    if (!inside_one(r.dk, bytes) || !inside_one(r.dv, bytes)) fail("staging outside the workspace");
+    const uintptr_t a = reinterpret_cast<uintptr_t>(r.dk), c = reinterpret_cast<uintptr_t>(r.dv);
+    if (a < c + bytes && c < a + bytes) fail("staged K and V overlap");
+    g_stage_lo = a < c ? a : c;
+    g_stage_hi = (a < c ? c : a) + bytes;
+}
+hipError_t launch_to_f16_kv(const StageReq& r, hipStream_t) {
+    ++g_launches;
+    check_stage(r);
+    return hipSuccess;
+}
 hipError_t launch_decode(const AttnArgs& a, int D, int G, hipStream_t) {
     common(a);
     if (a.n_split < 1 || a.n_split > kDecodeMaxSplit) fail("n_split out of range");
@@ -109,7 +123,8 @@ hipError_t launch_prefill(const AttnArgs& a, int, int, hipStream_t) {
     common(a);
     return hipSuccess;
 }
-hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t) {
+hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStream_t) {
+    if (stage) check_stage(*stage);
     common(a);
     if (a.mask) {
         const size_t bytes = (size_t)a.nq * a.hm * a.bm * 8;
@@ -132,18 +147,6 @@ hipError_t launch_zero(float* p, int64_t n, hipStream_t) {
 }
 hipError_t launch_kv_append(const AppendArgs&, hipStream_t) {
     ++g_launches;
-    return hipSuccess;
-}
-hipError_t launch_to_f16_kv(const float* k, int64_t, int64_t, int64_t, const float* v, int64_t, int64_t, int64_t,
-                            int d, int n, int h, int b, _Float16* dk, _Float16* dv, hipStream_t) {
-    ++g_launches;
-    const size_t bytes = (size_t)d * n * h * b * 2;
-    if (!k || !v) fail("staging source");
-    if (!inside_one(dk, bytes) || !inside_one(dv, bytes)) fail("staging outside the workspace");
-    const uintptr_t a = reinterpret_cast<uintptr_t>(dk), c = reinterpret_cast<uintptr_t>(dv);
-    if (a < c + bytes && c < a + bytes) fail("staged K and V overlap");
-    g_stage_lo = a < c ? a : c;
-    g_stage_hi = (a < c ? c : a) + bytes;
     return hipSuccess;
 }
 }  // namespace vxfa

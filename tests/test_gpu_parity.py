@@ -840,13 +840,16 @@ def test_ring_wrapped_with_appended_row_wrapping(runner):
 # --- the workspace: fixed at context creation, graph-safe ------------------------
 
 def test_graph_capture_then_larger_eager_calls(runner):
-    """A decode step captured into a HIP graph at n_kv 100 replays to the
-    eager bits after eager calls that use more splits and partial records
-    (n_kv 8192, 32 ragged streams), with eager work between the replays: no
-    call resizes, moves or leaves dirty the context's workspace."""
+    """A decode step captured into a HIP graph at n_kv 1024 (8 splits: its
+    partial records live in the context's workspace) replays to the eager
+    bits after eager calls that use more splits and records (n_kv 8192, 32
+    ragged streams), with eager work between the replays: no call resizes,
+    moves or leaves dirty the context's workspace. (Captures of F32 staging
+    and of the no-alloc scratch are in test_gpu_decode_layout.py and
+    test_zz_no_alloc.py.)"""
     import torch
     import gpu_util
-    small = cases.decode_case(100, seed=91)
+    small = cases.decode_case(1024, seed=91)
     dev = gpu_util.to_device(small)
     rc, ref = runner.run(small, dev=dev)
     assert rc == 0

@@ -148,3 +148,27 @@ def test_table_ranges_cover_live_blocks_and_copies_stay_in_bounds(nq, nkv):
             live = _live_blocks(table, range(qg * 128, min(qg * 128 + 128, nq)), nkv)
             assert set(range(blo, blo + nb)) == live, (name, qg, blo, nb)
         emulate_pp(sh, table=table)
+
+
+@pytest.mark.parametrize("stage_blocks,nrows", [(0, 1500), (375, 1500), (235, 1), (1, 17), (55, 439)])
+def test_prep_launch_partition(stage_blocks, nrows):
+    """prep_kernel (F32 staging and the mask pre-pass in one launch of
+    256-thread blocks): blocks [0, 2 sb) stage tensor bx / sb, block bx % sb;
+    the rest take 16 mask rows each, (bx - 2 sb) * 16 + tid / 16, rows past
+    nrows reading row nrows - 1 and storing nothing. Every staging block of
+    both tensors and every mask row is covered exactly once."""
+    sb = stage_blocks
+    nb = 2 * sb + (nrows + 15) // 16
+    staged, rows = [], []
+    for bx in range(nb):
+        if bx < 2 * sb:
+            staged.append((bx // sb, bx % sb))
+            continue
+        for tid in range(0, 256, 16):               # lane 0 of each row's 16 lanes stores
+            w = (bx - 2 * sb) * 16 + tid // 16
+            wr = min(w, nrows - 1)
+            assert 0 <= wr < nrows
+            if w < nrows:
+                rows.append(w)
+    assert sorted(staged) == [(t, b) for t in range(2) for b in range(sb)]
+    assert sorted(rows) == list(range(nrows))

@@ -106,6 +106,100 @@ struct DivMod {
     __host__ __device__ __forceinline__ uint32_t mod(uint32_t n) const { return n - d * f.div(n); }
 };
 
+// F32 -> f16 copies of the K and V views [d, n, h, b] (byte strides nb1..nb3,
+// rows contiguous) into contiguous [b][n][h][d] f16 buffers dk, dv
+struct StageReq {
+    const float* k;
+    int64_t k_nb1, k_nb2, k_nb3;
+    const float* v;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int d, n, h, b;
+    _Float16* dk;
+    _Float16* dv;
+};
+// The staging as launched: the flat index
+// of 8-element groups splits by shifts (d / 8 is a power of two) and
+// host-made reciprocals, all 32-bit; K is t = 0, V t = 1.
+struct StageArgs {
+    const float* src[2];
+    int64_t nb1[2], nb2[2], nb3[2];
+    _Float16* dst[2];
+    uint32_t total8;       // 8-element groups per tensor
+    uint32_t c8_log2;      // log2(d / 8)
+    DivMod h, n;
+};
+// Threads of a 256-thread block convert kStageUnits groups each, 256 groups
+// apart (2 x kStageUnits 16-byte loads in flight per thread).
+constexpr int kStageUnits = 4;
+constexpr uint32_t kStageGroupsPerBlock = 256u * kStageUnits;
+// Groups [bx * kStageGroupsPerBlock, + kStageGroupsPerBlock) of tensor t,
+// converted by thread `tid` of a 256-thread block. NT: nontemporal stores.
+template <bool NT>
+__device__ __forceinline__ void stage_groups(const StageArgs& sa, uint32_t bx, int t, uint32_t tid) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const uint32_t i0 = bx * kStageGroupsPerBlock + tid;
+    f4 x[kStageUnits][2];
+#pragma unroll
+    for (int u = 0; u < kStageUnits; ++u) {
+        const uint32_t i = min(i0 + 256u * u, sa.total8 - 1);   // past the end: reload the last group, store nothing
+        const uint32_t r = i >> sa.c8_log2;                     // row index (b, pos, h)
+        const uint32_t e = (i - (r << sa.c8_log2)) * 8;         // first element in the row
+        const uint32_t r2 = sa.h.div(r);
+        const uint32_t hh = r - r2 * sa.h.d;
+        const uint32_t bb = sa.n.div(r2);
+        const uint32_t pos = r2 - bb * sa.n.d;
+        const f4* p = (const f4*)((const char*)sa.src[t] + (int64_t)pos * sa.nb1[t] + (int64_t)hh * sa.nb2[t] +
+                                  (int64_t)bb * sa.nb3[t]) + e / 4;
+        x[u][0] = __builtin_nontemporal_load(p);
+        x[u][1] = __builtin_nontemporal_load(p + 1);
+    }
+#pragma unroll
+    for (int u = 0; u < kStageUnits; ++u) {
+        const uint32_t i = i0 + 256u * u;
+        h8 y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            y[j] = (_Float16)x[u][0][j];
+            y[4 + j] = (_Float16)x[u][1][j];
+        }
+        if (i < sa.total8) {
+            if constexpr (NT) __builtin_nontemporal_store(y, (h8*)(sa.dst[t] + (int64_t)i * 8));
+            else *(h8*)(sa.dst[t] + (int64_t)i * 8) = y;
+        }
+    }
+}
+// Host: the launch constants of a staging request (false: a shape the
+// kernel does not take, d / 8 not a power of two or over 2^31 groups), its
+// blocks per tensor, and whether its stores are nontemporal: copies of at
+// least 4 MiB (K and V) go past an XCD's L2 anyway, and nontemporal stores
+// leave no dirty lines to write back at the end of the launch (encoder F32
+// K/V 28.8 -> 28.4 us per layer, realtime encoder 52.7 -> 51.8); a small copy
+// (decoder prefill 439, 1.8 MB) keeps ordinary stores, which the next kernel
+// finds in L2 (19.8 us against 20.3 with nontemporal stores).
+inline bool make_stage_args(const StageReq& r, StageArgs& sa, uint32_t& blocks, bool& nt) {
+    if (r.d < 0 || r.d % 8 || (r.d / 8 & (r.d / 8 - 1)) || r.n < 0 || r.h < 0 || r.b < 0) return false;
+    const int64_t total8 = (int64_t)r.b * r.n * r.h * (r.d / 8);
+    if (total8 > 0x7fffff00) return false;
+    blocks = 0;
+    nt = false;
+    sa.total8 = 0;
+    if (total8 == 0) return true;   // nothing to launch
+    sa.src[0] = r.k; sa.src[1] = r.v;
+    sa.nb1[0] = r.k_nb1; sa.nb2[0] = r.k_nb2; sa.nb3[0] = r.k_nb3;
+    sa.nb1[1] = r.v_nb1; sa.nb2[1] = r.v_nb2; sa.nb3[1] = r.v_nb3;
+    sa.dst[0] = r.dk; sa.dst[1] = r.dv;
+    sa.total8 = (uint32_t)total8;
+    uint32_t l2 = 0;
+    while ((1 << l2) < r.d / 8) ++l2;
+    sa.c8_log2 = l2;
+    sa.h = DivMod::make((uint32_t)r.h);
+    sa.n = DivMod::make((uint32_t)(r.n > 0 ? r.n : 1));
+    blocks = (uint32_t)((total8 + kStageGroupsPerBlock - 1) / kStageGroupsPerBlock);
+    nt = (uint64_t)total8 * 32 >= ((uint64_t)4 << 20);
+    return true;
+}
+
 struct GridMap {
     uint32_t q8, r8;          // nwg / 8, nwg % 8
     uint32_t nqt, hq;
@@ -455,7 +549,10 @@ hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_
 // hd 64 prefill on the pipelined kernel: no mask, an implicit mask, or a mask
 // tensor (a.mask_rows: workspace for nq * hm * bm intervals, filled first by
 // a pre-pass launch)
-hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t stream);
+// stage: F32 K/V to convert first (a.k / a.v already point at the f16
+// copies), or null; with a mask tensor the conversion and the pre-pass share
+// one launch
+hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStream_t stream);
 // masked hd 128 prefill with n_kv <= 512 (a mask tensor or an implicit mask;
 // a rotary embedding of F32 Q)
 hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t stream);
@@ -463,9 +560,6 @@ hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t stream);
 bool prefill_pair_fits(const AttnArgs& a);
 hipError_t launch_zero(float* dst, int64_t n, hipStream_t stream);
 hipError_t launch_kv_append(const AppendArgs& a, hipStream_t stream);
-// F32 -> f16 copies of the K and V views [D, n, H, B] (byte strides nb1..nb3,
-// rows contiguous) into contiguous [B][n][H][D] f16 buffers, one launch
-hipError_t launch_to_f16_kv(const float* k, int64_t k_nb1, int64_t k_nb2, int64_t k_nb3, const float* v,
-                            int64_t v_nb1, int64_t v_nb2, int64_t v_nb3, int d, int n, int h, int b, _Float16* dk,
-                            _Float16* dv, hipStream_t stream);
+// F32 -> f16 copies of K and V (StageReq above), one launch of their own
+hipError_t launch_to_f16_kv(const StageReq& r, hipStream_t stream);
 }  // namespace vxfa

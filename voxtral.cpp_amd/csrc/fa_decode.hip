@@ -751,75 +751,23 @@ hipError_t launch_zero(float* dst, int64_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
-// F32 -> f16 (round to nearest even) copies of the K and V views [d, n, h, b]
-// into contiguous [b][n][h][d] buffers, both in one launch: blockIdx.y picks
-// K or V, each thread converts 8 consecutive elements (two 16-byte loads, one
-// 16-byte store). The flat index splits by shifts (d / 8 is a power of two)
-// and host-made reciprocals, all 32-bit. Used to stage F32 K/V for the
-// prefill kernels, whose tiles reach LDS by direct global-to-LDS copies.
-struct StageArgs {
-    const float* src[2];
-    int64_t nb1[2], nb2[2], nb3[2];
-    _Float16* dst[2];
-    uint32_t total8;       // 8-element groups per tensor
-    uint32_t c8_log2;      // log2(d / 8)
-    DivMod h, n;
-};
-
-// Each thread converts kStageUnits groups of 8 elements, 256 groups apart
-// (2 x kStageUnits 16-byte loads in flight per thread).
-constexpr int kStageUnits = 4;
+// F32 -> f16 (round to nearest even) copies of K and V for the prefill
+// kernels, whose tiles reach LDS by direct global-to-LDS copies: one launch,
+// blockIdx.y picks K or V (the staging body, stage_groups, is in fa_common.h).
+template <bool NT>
 __global__ __launch_bounds__(256) void to_f16_kv_kernel(StageArgs sa) {
-    const int t = blockIdx.y;
-    const uint32_t i0 = blockIdx.x * (256u * kStageUnits) + threadIdx.x;
-    floatx4 x[kStageUnits][2];
-#pragma unroll
-    for (int u = 0; u < kStageUnits; ++u) {
-        const uint32_t i = min(i0 + 256u * u, sa.total8 - 1);   // past the end: reload the last group, store nothing
-        const uint32_t r = i >> sa.c8_log2;                     // row index (b, pos, h)
-        const uint32_t e = (i - (r << sa.c8_log2)) * 8;         // first element in the row
-        const uint32_t r2 = sa.h.div(r);
-        const uint32_t hh = r - r2 * sa.h.d;
-        const uint32_t bb = sa.n.div(r2);
-        const uint32_t pos = r2 - bb * sa.n.d;
-        const floatx4* p = (const floatx4*)((const char*)sa.src[t] + (int64_t)pos * sa.nb1[t] +
-                                            (int64_t)hh * sa.nb2[t] + (int64_t)bb * sa.nb3[t]) + e / 4;
-        x[u][0] = __builtin_nontemporal_load(p);
-        x[u][1] = __builtin_nontemporal_load(p + 1);
-    }
-#pragma unroll
-    for (int u = 0; u < kStageUnits; ++u) {
-        const uint32_t i = i0 + 256u * u;
-        half8 y;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            y[j] = (_Float16)x[u][0][j];
-            y[4 + j] = (_Float16)x[u][1][j];
-        }
-        if (i < sa.total8) *(half8*)(sa.dst[t] + (int64_t)i * 8) = y;
-    }
+    stage_groups<NT>(sa, blockIdx.x, (int)blockIdx.y, threadIdx.x);
 }
 
-hipError_t launch_to_f16_kv(const float* k, int64_t k_nb1, int64_t k_nb2, int64_t k_nb3, const float* v, int64_t v_nb1,
-                            int64_t v_nb2, int64_t v_nb3, int d, int n, int h, int b, _Float16* dk, _Float16* dv,
-                            hipStream_t st) {
-    if (d % 8 || (d / 8 & (d / 8 - 1)) || n < 0 || h < 0 || b < 0) return hipErrorInvalidValue;
-    const int64_t total8 = (int64_t)b * n * h * (d / 8);
-    if (total8 == 0) return hipSuccess;
-    if (total8 > 0x7fffff00) return hipErrorInvalidValue;
+hipError_t launch_to_f16_kv(const StageReq& r, hipStream_t st) {
     StageArgs sa;
-    sa.src[0] = k; sa.src[1] = v;
-    sa.nb1[0] = k_nb1; sa.nb2[0] = k_nb2; sa.nb3[0] = k_nb3;
-    sa.nb1[1] = v_nb1; sa.nb2[1] = v_nb2; sa.nb3[1] = v_nb3;
-    sa.dst[0] = dk; sa.dst[1] = dv;
-    sa.total8 = (uint32_t)total8;
-    uint32_t l2 = 0;
-    while ((1 << l2) < d / 8) ++l2;
-    sa.c8_log2 = l2;
-    sa.h = DivMod::make((uint32_t)h);
-    sa.n = DivMod::make((uint32_t)n);
-    const dim3 grid((unsigned)((total8 + 256 * kStageUnits - 1) / (256 * kStageUnits)), 2);
-    hipLaunchKernelGGL(to_f16_kv_kernel, grid, dim3(256), 0, st, sa);
+    uint32_t blocks = 0;
+    bool nt = false;
+    if (!make_stage_args(r, sa, blocks, nt)) return hipErrorInvalidValue;
+    if (sa.total8 == 0) return hipSuccess;
+    const dim3 grid(blocks, 2);
+    if (nt) hipLaunchKernelGGL(to_f16_kv_kernel<true>, grid, dim3(256), 0, st, sa);
+    else hipLaunchKernelGGL(to_f16_kv_kernel<false>, grid, dim3(256), 0, st, sa);
     return hipGetLastError();
 }
 

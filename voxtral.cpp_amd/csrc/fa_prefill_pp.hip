@@ -189,7 +189,9 @@ __device__ __forceinline__ int row16_sum_i(int x) {
 
 // The pre-pass of a mask tensor: 16 lanes (one DPP row) per mask row
 // w = (batch bm_i, plane p, row q), w = (bm_i * hm + p) * nq + q, 4 rows per
-// single-wavefront workgroup; writes out[w] = {lo, hi} when the row's entries
+// single-wavefront workgroup (mask_rows_kernel), or 16 per 256-thread block
+// in the launch that also stages F32 K/V (prep_kernel); writes out[w] =
+// {lo, hi} when the row's entries
 // are 0 (+0 or -0) on [lo, hi] and -inf elsewhere, {n, -1} when every entry
 // is -inf, {-2, -2} otherwise. The row is read as the 16-byte-aligned chunks
 // that cover it (any row alignment; a chunk holds at least one byte of the
@@ -202,15 +204,20 @@ __device__ __forceinline__ int row16_sum_i(int x) {
 // an interval iff the count is hi - lo + 1), reduced over the row's 16 lanes
 // with DPP rotates.
 constexpr int kMaskRowChunks = 12;   // chunks per lane per round
-__global__ __launch_bounds__(64) void mask_rows_kernel(const uint16_t* mask, int64_t nb1, int64_t nb2, int64_t nb3,
-                                                       int n, int nq, int hm, int nrows, int2* out) {
-    const int s = threadIdx.x & 15;
-    const int w = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 4);
-    const int wr = min(w, nrows - 1);   // a row group past the last row reads the last row, writes nothing
-    const int q = wr % nq, pb = wr / nq, p = pb % hm, bb = pb / hm;
-    const char* rowp = (const char*)mask + (int64_t)q * nb1 + (int64_t)p * nb2 + (int64_t)bb * nb3;
+struct MaskRowArgs {
+    const uint16_t* mask;
+    int64_t nb1, nb2, nb3;
+    int n, nq, hm, nrows;
+    int2* out;
+};
+// Mask row w (w < nrows) by lane s (0..15) of its 16-lane DPP row; every lane
+// of the row calls it (rows past nrows pass w = nrows - 1 and store nothing).
+__device__ __forceinline__ void mask_row_interval(const MaskRowArgs& m, int w, int s, bool store) {
+    const int q = w % m.nq, pb = w / m.nq, p = pb % m.hm, bb = pb / m.hm;
+    const char* rowp = (const char*)m.mask + (int64_t)q * m.nb1 + (int64_t)p * m.nb2 + (int64_t)bb * m.nb3;
     const int mis = (int)(reinterpret_cast<uintptr_t>(rowp) & 15);   // even: the mask is 2-byte aligned
     const char* base = rowp - mis;
+    const int n = m.n;
     const int nch = (mis + 2 * n + 15) / 16;
     const int nchmax = (14 + 2 * n + 15) / 16;                         // the same loop for every row
     int lo = 0x7fffffff, hi = -1, cnt = 0;
@@ -245,8 +252,27 @@ __global__ __launch_bounds__(64) void mask_rows_kernel(const uint16_t* mask, int
     hi = row16_max_i(hi);
     cnt = row16_sum_i(cnt);
     const int nonzero = row16_max_i(nzall != 0 ? 1 : 0);
-    if (s == 0 && w < nrows)
-        out[w] = hi < lo ? int2{n, -1} : ((nonzero || cnt != hi - lo + 1) ? int2{-2, -2} : int2{lo, hi});
+    if (s == 0 && store)
+        m.out[w] = hi < lo ? int2{n, -1} : ((nonzero || cnt != hi - lo + 1) ? int2{-2, -2} : int2{lo, hi});
+}
+
+__global__ __launch_bounds__(64) void mask_rows_kernel(MaskRowArgs m) {
+    const int w = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 4);
+    mask_row_interval(m, min(w, m.nrows - 1), (int)(threadIdx.x & 15), w < m.nrows);
+}
+
+// F32 K/V staging and the mask pre-pass in one launch of 256-thread blocks:
+// blocks [0, 2 sb) stage K (the first sb) and V, the rest find the intervals
+// of 16 mask rows each.
+template <bool NT>
+__global__ __launch_bounds__(256) void prep_kernel(StageArgs sa, uint32_t sb, MaskRowArgs m) {
+    const uint32_t bx = blockIdx.x;
+    if (bx < 2 * sb) {
+        stage_groups<NT>(sa, bx % sb, (int)(bx / sb), threadIdx.x);
+        return;
+    }
+    const int w = (int)(bx - 2 * sb) * 16 + (int)(threadIdx.x >> 4);
+    mask_row_interval(m, min(w, m.nrows - 1), (int)(threadIdx.x & 15), w < m.nrows);
 }
 
 template <bool QF16, bool C8, int MM>
@@ -886,7 +912,7 @@ static void launch_pp_mm(const AttnArgs& a, const GridMap& gm, int nblk, int ni,
     }
 }
 
-hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
+hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStream_t st) {
     using namespace pp;
     const int nqg = (a.nq + BM - 1) / BM;
     const int nblk = (a.nkv + BK - 1) / BK;
@@ -898,17 +924,31 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, hipStream_t st) {
     const bool is_c8 = fabsf(a.scale_log2) == c8 && __builtin_bit_cast(uint32_t, c8) == 0x3e38aa3bu;
     const GridMap gm = GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
+    StageArgs sa;
+    uint32_t sb = 0;
+    bool snt = false;
+    if (stage && !make_stage_args(*stage, sa, sb, snt)) return hipErrorInvalidValue;
     if (a.mask) {
         if (!a.mask_rows) return hipErrorInvalidValue;
         const int64_t nrows = (int64_t)a.nq * a.hm * a.bm;
-        if (nrows > 0x7fffffff - 3) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(mask_rows_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(64), 0, st, a.mask, a.m_nb1,
-                           a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows);
+        if (nrows > 0x7fffffff - 15) return hipErrorInvalidValue;
+        const MaskRowArgs m{a.mask, a.m_nb1, a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows};
+        if (sb > 0) {
+            const uint64_t nb = 2ull * sb + (uint64_t)((nrows + 15) / 16);
+            if (nb > 0x7fffffffull) return hipErrorInvalidValue;
+            if (snt) hipLaunchKernelGGL(prep_kernel<true>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, m);
+            else hipLaunchKernelGGL(prep_kernel<false>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, m);
+        } else {
+            hipLaunchKernelGGL(mask_rows_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(64), 0, st, m);
+        }
         launch_pp_mm<1>(a, gm, nblk, ni, is_c8, grid, block, st);
-    } else if (a.im_causal) {
-        launch_pp_mm<2>(a, gm, nblk, ni, is_c8, grid, block, st);
     } else {
-        launch_pp_mm<0>(a, gm, nblk, ni, is_c8, grid, block, st);
+        if (sb > 0) {
+            const hipError_t e = launch_to_f16_kv(*stage, st);
+            if (e != hipSuccess) return e;
+        }
+        if (a.im_causal) launch_pp_mm<2>(a, gm, nblk, ni, is_c8, grid, block, st);
+        else launch_pp_mm<0>(a, gm, nblk, ni, is_c8, grid, block, st);
     }
     return hipGetLastError();
 }

@@ -485,11 +485,13 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
         size_t staged = 0;   // bytes of the staging area this call fills
+        vxfa::StageReq stage;
         if (a.kv_f32) {
             // F32 K/V (the reference's own cache and encoder K/V): an f16 copy
             // in the context's staging area, [Bk][Nkv][Hkv][D], read by the
             // prefill kernels like any f16 view (their tiles reach LDS by
-            // direct global-to-LDS copies, which cannot convert)
+            // direct global-to-LDS copies, which cannot convert); launched
+            // below, with the kernel that reads it
             const int64_t Bk = k->ne[3];
             const int64_t per = Bk * Nkv * Hkv * D;
             if ((size_t)(2 * per) * sizeof(_Float16) > w.stage_bytes) {
@@ -499,11 +501,10 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             }
             _Float16* sk = w.stage;
             _Float16* sv = w.stage + per;
-            e = vxfa::launch_to_f16_kv(static_cast<const float*>(k->data), (int64_t)k->nb[1], (int64_t)k->nb[2],
-                                       (int64_t)k->nb[3], static_cast<const float*>(v->data), (int64_t)v->nb[1],
-                                       (int64_t)v->nb[2], (int64_t)v->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sk,
-                                       sv, st);
-            if (e != hipSuccess) { set_err(w, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+            stage = vxfa::StageReq{static_cast<const float*>(k->data), (int64_t)k->nb[1], (int64_t)k->nb[2],
+                                   (int64_t)k->nb[3], static_cast<const float*>(v->data), (int64_t)v->nb[1],
+                                   (int64_t)v->nb[2], (int64_t)v->nb[3], (int)D, (int)Nkv, (int)Hkv, (int)Bk, sk,
+                                   sv};
             staged = (size_t)(2 * per) * sizeof(_Float16);
             a.k = sk;
             a.v = sv;
@@ -530,20 +531,27 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel, also under
             // an implicit causal / window mask or a mask tensor (the realtime
-            // encoder's window)
-            e = vxfa::launch_prefill64_pp(a, st);
-        } else if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled && vxfa::prefill_pair_fits(a)) {
-            // short masked prefill (voxtral's decoder prefill): paired query
-            // tiles, every live block on its own wavefront
-            e = vxfa::launch_prefill_pair(a, st);
+            // encoder's window); it launches the F32 staging itself, in the mask
+            // pre-pass's launch when there is one
+            e = vxfa::launch_prefill64_pp(a, staged ? &stage : nullptr, st);
         } else {
-            // query-row wavefronts per workgroup (each with its KV partner
-            // wavefronts): 4 shares every staged K/V step among 128 query rows;
-            // hd 128 and small grids (fewer than 128 workgroups of 128 rows) use 2
-            const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
-            int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
-            if (w.tune.waves_override == 2 || w.tune.waves_override == 4) waves = w.tune.waves_override;
-            e = vxfa::launch_prefill(a, (int)D, waves, st);
+            if (staged) {
+                e = vxfa::launch_to_f16_kv(stage, st);
+                if (e != hipSuccess) { set_err(w, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+            }
+            if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled && vxfa::prefill_pair_fits(a)) {
+                // short masked prefill (voxtral's decoder prefill): paired query
+                // tiles, every live block on its own wavefront
+                e = vxfa::launch_prefill_pair(a, st);
+            } else {
+                // query-row wavefronts per workgroup (each with its KV partner
+                // wavefronts): 4 shares every staged K/V step among 128 query rows;
+                // hd 128 and small grids (fewer than 128 workgroups of 128 rows) use 2
+                const int64_t wg4 = ((Nq + 127) / 128) * Hq * B;
+                int waves = (D == 64 && wg4 >= 128) ? 4 : 2;
+                if (w.tune.waves_override == 2 || w.tune.waves_override == 4) waves = w.tune.waves_override;
+                e = vxfa::launch_prefill(a, (int)D, waves, st);
+            }
         }
     }
     if (e != hipSuccess) {
