@@ -72,6 +72,40 @@ int main() {
             ++checks;
         }
     }
+    // the heavy-first order (make_tiles_desc) where hq * B is a multiple of 8:
+    // XCD x = lin % 8 takes pairs t in [x hx, (x + 1) hx), tile nqt - 1 - j / hx
+    // for j = lin / 8, t = x hx + j % hx; a bijection onto the (qt, h, b) triples
+    const int dshapes[][5] = {{12, 32, 1, 32, 1}, {12, 20, 2, 20, 2}, {1, 8, 1, 8, 1}, {5, 16, 3, 4, 3},
+                              {24, 32, 1, 8, 1}, {3, 4, 2, 2, 1}, {12, 20, 1, 20, 1}};
+    for (auto& s : dshapes) {
+        const int nqt = s[0], hq = s[1], B = s[2], hkv = s[3], bk = s[4];
+        const int nwg = nqt * hq * B;
+        const GridMap g = GridMap::make_tiles_desc(nwg, nqt, hq, hkv, B, bk);
+        const bool desc = (hq * B) % 8 == 0;
+        if ((g.hx != 0) != desc) return fail("desc eligibility", hq, B, g.hx);
+        const int hx = hq * B / 8;
+        std::vector<int> seen((size_t)nwg, 0);
+        for (int lin = 0; lin < nwg; ++lin) {
+            int qt, h, b, hk, bkv;
+            g.locate((uint32_t)lin, qt, h, b, hk, bkv);
+            int wqt, wt;
+            if (desc) {
+                const int x = lin & 7, j = lin >> 3;
+                wqt = nqt - 1 - j / hx;
+                wt = x * hx + j % hx;
+            } else {
+                const int q8 = nwg >> 3, r8 = nwg & 7, xcd = lin & 7;
+                const int gidx = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + (lin >> 3);
+                wqt = gidx % nqt;
+                wt = gidx / nqt;
+            }
+            if (qt != wqt || h != wt % hq || b != wt / hq) return fail("locate desc", lin, qt, wqt);
+            if (hk != h / (hq / hkv) || bkv != b / (B / bk)) return fail("locate desc kv", lin, hk, bkv);
+            const int gi = (b * hq + h) * nqt + qt;
+            if (qt < 0 || qt >= nqt || gi < 0 || gi >= nwg || seen[gi]++) return fail("bijection desc", lin, gi, nwg);
+            ++checks;
+        }
+    }
     // staging index (to_f16_kv_kernel): i -> r = i >> log2(d/8), e = 8 (i - r (d/8)),
     // hh = r % h, pos = (r / h) % n, bb = r / h / n; element 8 i of the buffer
     const int stg[][4] = {{64, 1500, 20, 1}, {128, 439, 8, 1}, {64, 7, 3, 5}, {128, 8192, 8, 2}, {64, 1, 1, 1}};

@@ -204,16 +204,43 @@ struct GridMap {
     uint32_t q8, r8;          // nwg / 8, nwg % 8
     uint32_t nqt, hq;
     FastDiv by_nqt, by_hq, by_grp, by_bgrp;   // grp = hq / hkv, bgrp = b / bk
+    // Heavy tiles first (hx > 0; masked prefill, where a causal or window
+    // mask makes later query tiles longer): XCD x takes the (batch, head)
+    // pairs t = b hq + h in [x hx, (x + 1) hx), hx = hq b / 8, and deals its
+    // workgroups query tile by query tile from the last: lin / 8 = j gives
+    // qt = nqt - 1 - j / hx, t = x hx + j % hx. The heads of one XCD still
+    // share its L2, and the first round of workgroups (those dispatched
+    // before any ends) holds the longest walks.
+    uint32_t hx;
+    FastDiv by_hx;
     static GridMap make(int nwg, int nqt, int hq, int hkv, int b, int bk) {
         return GridMap{(uint32_t)nwg >> 3, (uint32_t)nwg & 7, (uint32_t)nqt, (uint32_t)hq,
-                       FastDiv::make(nqt), FastDiv::make(hq), FastDiv::make(hq / hkv), FastDiv::make(b / bk)};
+                       FastDiv::make(nqt), FastDiv::make(hq), FastDiv::make(hq / hkv), FastDiv::make(b / bk),
+                       0u, FastDiv::make(1)};
+    }
+    // the heavy-first order where hq * b is a multiple of 8, else make()'s
+    static GridMap make_tiles_desc(int nwg, int nqt, int hq, int hkv, int b, int bk) {
+        GridMap g = make(nwg, nqt, hq, hkv, b, bk);
+        if ((hq * b) % 8 == 0) {
+            g.hx = (uint32_t)(hq * b / 8);
+            g.by_hx = FastDiv::make(g.hx);
+        }
+        return g;
     }
     __host__ __device__ __forceinline__ void locate(uint32_t lin, int& qt, int& h, int& b, int& hk, int& bkv) const {
         const uint32_t xcd = lin & 7;
-        const uint32_t gidx = (xcd < r8 ? xcd : r8) * (q8 + 1) + (xcd > r8 ? xcd - r8 : 0u) * q8 + (lin >> 3);
-        const uint32_t t = by_nqt.div(gidx);
+        uint32_t t;
+        if (hx) {
+            const uint32_t j = lin >> 3;
+            const uint32_t jt = by_hx.div(j);
+            qt = (int)(nqt - 1 - jt);
+            t = xcd * hx + (j - jt * hx);
+        } else {
+            const uint32_t gidx = (xcd < r8 ? xcd : r8) * (q8 + 1) + (xcd > r8 ? xcd - r8 : 0u) * q8 + (lin >> 3);
+            t = by_nqt.div(gidx);
+            qt = (int)(gidx - t * nqt);
+        }
         const uint32_t bb = by_hq.div(t);
-        qt = (int)(gidx - t * nqt);
         h = (int)(t - bb * hq);
         b = (int)bb;
         hk = (int)by_grp.div((uint32_t)h);

@@ -807,7 +807,10 @@ static hipError_t launch_pw(const AttnArgs& a, hipStream_t st) {
     const int64_t nwg = (int64_t)nqt * a.hq * a.b;
     if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
     constexpr int NT = 64 * NQW * KVG;
-    const GridMap gm = GridMap::make((int)nwg, nqt, a.hq, a.hkv, a.b, a.bk);
+    // under a mask, heavy query tiles first (a causal or window mask makes
+    // later tiles walk more steps)
+    const GridMap gm = MM != 0 ? GridMap::make_tiles_desc((int)nwg, nqt, a.hq, a.hkv, a.b, a.bk)
+                               : GridMap::make((int)nwg, nqt, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
     if (a.q_f16) hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, true>), grid, block, 0, st, a, gm);
     else hipLaunchKernelGGL((fa_prefill_kernel<D, NQW, KVG, MM, false>), grid, block, 0, st, a, gm);

@@ -922,7 +922,10 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStre
     // |scale| * log2(e) equal, bit for bit, to the literal in the kernel
     const float c8 = 0.125f * kLog2e;
     const bool is_c8 = fabsf(a.scale_log2) == c8 && __builtin_bit_cast(uint32_t, c8) == 0x3e38aa3bu;
-    const GridMap gm = GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
+    // under a mask, heavy query tiles first (a causal or window mask makes
+    // later tiles walk more blocks)
+    const GridMap gm = (a.mask || a.im_causal) ? GridMap::make_tiles_desc((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk)
+                                               : GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
     StageArgs sa;
     uint32_t sb = 0;
