@@ -91,14 +91,17 @@ def test_decode_split_counts(runners, name, splits):
 
 
 def test_graph_capture_with_split_records(runners):
-    """decode n_kv 8192 (64 records per pair), n_kv 1024 (8) and an F32 K/V
-    prefill (staging) captured together; replayed three times with eager
-    calls of other shapes between the replays"""
+    """decode n_kv 8192 (64 records per pair), n_kv 1024 (8), an F32 K/V
+    prefill (staging) and an hd 64 F32 K/V prefill with a window mask tensor
+    (staging and the mask pre-pass in one launch, the interval table in the
+    record region) captured together; replayed three times with eager calls
+    of other shapes between the replays"""
     import torch
     import gpu_util
     r = runners["default"]
     cs = [cases.decode_case(8192, seed=541), cases.decode_case(1024, seed=542),
-          cases.prefill_case(200, seed=543, kv_f32=True)]
+          cases.prefill_case(200, seed=543, kv_f32=True),
+          cases.encoder_case(500, 8, 64, seed=544, window=200, kv_f32=True)]
     devs = [gpu_util.to_device(c) for c in cs]
     eager = []
     outs = []

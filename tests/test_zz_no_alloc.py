@@ -77,15 +77,18 @@ def test_noalloc_rejects_staging_beyond_the_scratch(runner):
 
 def test_noalloc_graph_capture_replays(runner):
     """No-alloc calls captured into a HIP graph, after eager no-alloc calls on
-    the device (the first call on a device looks up the scratch and checks
-    the XCD mapping, which synchronises, so it is made outside capture):
-    decode n_kv 8192 (split records and arrival counters in the scratch) and
-    an F32 K/V prefill (f16 staging in the scratch). Three replays, each
-    followed by eager no-alloc calls of other shapes, match the eager bits."""
+    the device (the first call on a device looks up the scratch, which may
+    load the code object, so it is made outside capture): decode n_kv 8192
+    (split records in the scratch), an F32 K/V prefill (f16 staging in the
+    scratch) and an hd 64 F32 K/V prefill with a window mask tensor (staging
+    and the mask pre-pass in one launch, the interval table after the staged
+    K/V). Three replays, each followed by eager no-alloc calls of other
+    shapes, match the eager bits."""
     import torch
     import gpu_util
     vx = gpu_util.vxfa
-    cs = [cases.decode_case(8192, seed=311), cases.prefill_case(300, seed=312, kv_f32=True)]
+    cs = [cases.decode_case(8192, seed=311), cases.prefill_case(300, seed=312, kv_f32=True),
+          cases.encoder_case(600, 8, 64, seed=316, window=300, kv_f32=True)]
     devs = [gpu_util.to_device(c) for c in cs]
     eager = []
     for c, d in zip(cs, devs):
