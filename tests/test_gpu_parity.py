@@ -412,12 +412,14 @@ HD64_MASK_BITWISE = True
 
 @pytest.mark.parametrize("seq,heads,window,offset", [(1500, 4, 750, 0), (1500, 2, 0, 0), (333, 3, 1, 0),
                                                      (257, 2, 31, 5), (700, 2, 100, 600), (129, 2, 0, -100),
-                                                     (64, 1, 33, 0), (1, 2, 0, 0), (161, 2, 64, 0)])
+                                                     (64, 1, 33, 0), (1, 2, 0, 0), (161, 2, 64, 0),
+                                                     (700, 8, 200, 0), (300, 16, 0, 50)])
 def test_implicit_hd64_windows(runner, seq, heads, window, offset):
     """The pipelined hd 64 kernel under implicit causal / window masks: row
     ranges that start and end inside a block, windows of one position and of
     one block less one, offsets past the KV length and before it (rows with
-    no live position give zeros), partial last blocks."""
+    no live position give zeros), partial last blocks; 8 and 16 heads take
+    the heavy-tiles-first grid order."""
     from conftest import load_package
     import gpu_util
     vx = load_package().vxfa
