@@ -147,10 +147,11 @@ NEG_INF_F16 = 0xFC00
 def mask_row_interval(row, mis):
     """The pre-pass of a mask tensor (mask_rows_kernel) for one F16 mask row
     (uint16 array of n entries) whose first entry sits mis bytes (even, < 16)
-    past a 16-byte boundary: 16 lanes read 16-byte chunks from the boundary,
-    lane s of round c0 (c0 = 0, 192, ... below nchmax, the chunk count of the
-    worst alignment) chunk min(c0 + 16 u + s, nch - 1) for u < 12, entry e
-    of chunk slot c being column 8 c - mis / 2 + e; the entries of
+    past a 16-byte boundary: the row's 64 lanes read 16-byte chunks from the
+    boundary, lane s of round c0 (c0 = 0, 192, ... below nchmax, the chunk
+    count of the worst alignment) chunk min(c0 + 64 u + s, nch - 1) for
+    u < 3, entry e of chunk slot c being column 8 c - mis / 2 + e; the
+    entries of
     [elo, ehi) (those in [0, n)) count, through bit masks: live (in the row,
     not -inf) and nz (live and non-zero). From the first and last live
     columns lo and hi, their count and whether one is non-zero it returns
@@ -163,10 +164,10 @@ def mask_row_interval(row, mis):
     _check(nch <= nchmax, "the row has more chunks than the loop walks")
     lo, hi, cnt, nonzero = 1 << 31, -1, 0, False
     counted = []
-    for c0 in range(0, nchmax, 16 * 12):
-        for u in range(12):
-            for s in range(16):
-                c = c0 + 16 * u + s
+    for c0 in range(0, nchmax, 64 * 3):
+        for u in range(3):
+            for s in range(64):
+                c = c0 + 64 * u + s
                 ld = min(c, nch - 1)             # the chunk the lane loads
                 _check(0 <= ld < nch, "a load outside the row's chunks")
                 col0 = 8 * c - mis // 2

@@ -152,20 +152,24 @@ def test_table_ranges_cover_live_blocks_and_copies_stay_in_bounds(nq, nkv):
 
 @pytest.mark.parametrize("stage_blocks,nrows", [(0, 1500), (375, 1500), (235, 1), (1, 17), (55, 439)])
 def test_prep_launch_partition(stage_blocks, nrows):
-    """prep_kernel (F32 staging and the mask pre-pass in one launch of
-    256-thread blocks): blocks [0, 2 sb) stage tensor bx / sb, block bx % sb;
-    the rest take 16 mask rows each, (bx - 2 sb) * 16 + tid / 16, rows past
-    nrows reading row nrows - 1 and storing nothing. Every staging block of
-    both tensors and every mask row is covered exactly once."""
+    """prep_kernel (the mask pre-pass and F32 staging in one launch of
+    256-thread blocks): blocks [0, nmb) take four mask rows each, one per
+    wavefront, bx * 4 + tid / 64, rows past nrows reading row nrows - 1 and
+    storing nothing; blocks [nmb, nmb + 2 sb) stage tensor (bx - nmb) / sb,
+    block (bx - nmb) % sb. mask_rows_kernel is the first part alone. Every
+    staging block of both tensors and every mask row is covered exactly
+    once."""
     sb = stage_blocks
-    nb = 2 * sb + (nrows + 15) // 16
+    nmb = (nrows + 3) // 4
+    nb = nmb + 2 * sb
     staged, rows = [], []
     for bx in range(nb):
-        if bx < 2 * sb:
-            staged.append((bx // sb, bx % sb))
+        if bx >= nmb:
+            sx = bx - nmb
+            staged.append((sx // sb, sx % sb))
             continue
-        for tid in range(0, 256, 16):               # lane 0 of each row's 16 lanes stores
-            w = (bx - 2 * sb) * 16 + tid // 16
+        for tid in range(0, 256, 64):               # lane 0 of each row's wavefront stores
+            w = bx * 4 + tid // 64
             wr = min(w, nrows - 1)
             assert 0 <= wr < nrows
             if w < nrows:

@@ -190,31 +190,53 @@ __device__ __forceinline__ int row16_sum_i(int x) {
     return x + __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false);
 }
 
-// The pre-pass of a mask tensor: 16 lanes (one DPP row) per mask row
-// w = (batch bm_i, plane p, row q), w = (bm_i * hm + p) * nq + q, 4 rows per
-// single-wavefront workgroup (mask_rows_kernel), or 16 per 256-thread block
-// in the launch that also stages F32 K/V (prep_kernel); writes out[w] =
-// {lo, hi} when the row's entries
-// are 0 (+0 or -0) on [lo, hi] and -inf elsewhere, {n, -1} when every entry
-// is -inf, {-2, -2} otherwise. The row is read as the 16-byte-aligned chunks
-// that cover it (any row alignment; a chunk holds at least one byte of the
-// row, so it lies in the same granule as mask data): in rounds of 192
-// chunks, lane s of the row loading chunks c0 + 16 u + s (u < 12, all in
-// flight; a chunk past the row's last reloads the last and counts nothing).
-// Branch-free per chunk: bit e of `live` is set when entry e lies in the row
-// and is not -inf, of `nz` when it is also non-zero; one pass gives the first
-// and last live column, their count and whether one is non-zero (the row is
-// an interval iff the count is hi - lo + 1), reduced over the row's 16 lanes
-// with DPP rotates.
-constexpr int kMaskRowChunks = 12;   // chunks per lane per round
+// min / max / sum over the 64 lanes: DPP row reductions, then the four rows'
+// results read into scalar registers (uniform result, no LDS traffic)
+__device__ __forceinline__ int wave_min_dpp(int x) {
+    x = row16_min_i(x);
+    return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+__device__ __forceinline__ int wave_max_dpp(int x) {
+    x = row16_max_i(x);
+    return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+__device__ __forceinline__ int wave_sum_dpp(int x) {
+    x = row16_sum_i(x);
+    return (__builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16)) +
+           (__builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48));
+}
+
+// The pre-pass of a mask tensor: one wavefront per mask row
+// w = (batch bm_i, plane p, row q), w = (bm_i * hm + p) * nq + q, four rows
+// per 256-thread block (mask_rows_kernel, and the first blocks of the launch
+// that also stages F32 K/V, prep_kernel); writes out[w] = {lo, hi} when the
+// row's entries are 0 (+0 or -0) on [lo, hi] and -inf elsewhere, {n, -1}
+// when every entry is -inf, {-2, -2} otherwise. The row is read as the
+// 16-byte-aligned chunks that cover it (any row alignment; a chunk holds at
+// least one byte of the row, so it lies in the same granule as mask data):
+// in rounds of 192 chunks, lane s loading chunks c0 + 64 u + s (u < 3, all
+// in flight; a chunk past the row's last reloads the last and counts
+// nothing). Branch-free per chunk: bit e of `live` is set when entry e lies
+// in the row and is not -inf, of `nz` when it is also non-zero; one pass
+// gives the first and last live column, their count and whether one is
+// non-zero (the row is an interval iff the count is hi - lo + 1), reduced
+// over the wavefront. A whole wavefront per row, not a 16-lane DPP row: the
+// pre-pass is bound by its VALU work per lane, which a single wavefront per
+// SIMD issues at about half the SIMD's rate (1500 realtime-encoder rows:
+// 4.8 us with 16 lanes and 12 chunks per lane).
+constexpr int kMaskRowChunks = 3;    // chunks per lane per round
+constexpr int kMaskRowRound = 64 * kMaskRowChunks;
 struct MaskRowArgs {
     const uint16_t* mask;
     int64_t nb1, nb2, nb3;
     int n, nq, hm, nrows;
     int2* out;
 };
-// Mask row w (w < nrows) by lane s (0..15) of its 16-lane DPP row; every lane
-// of the row calls it (rows past nrows pass w = nrows - 1 and store nothing).
+// Mask row w (w < nrows, uniform over the wavefront) by lane s (0..63);
+// every lane calls it (waves past the last row pass w = nrows - 1 and store
+// nothing).
 __device__ __forceinline__ void mask_row_interval(const MaskRowArgs& m, int w, int s, bool store) {
     const int q = w % m.nq, pb = w / m.nq, p = pb % m.hm, bb = pb / m.hm;
     const char* rowp = (const char*)m.mask + (int64_t)q * m.nb1 + (int64_t)p * m.nb2 + (int64_t)bb * m.nb3;
@@ -225,13 +247,13 @@ __device__ __forceinline__ void mask_row_interval(const MaskRowArgs& m, int w, i
     const int nchmax = (14 + 2 * n + 15) / 16;                         // the same loop for every row
     int lo = 0x7fffffff, hi = -1, cnt = 0;
     uint32_t nzall = 0;
-    for (int c0 = 0; c0 < nchmax; c0 += 16 * kMaskRowChunks) {
+    for (int c0 = 0; c0 < nchmax; c0 += kMaskRowRound) {
         u32x4 wv[kMaskRowChunks];
 #pragma unroll
-        for (int u = 0; u < kMaskRowChunks; ++u) wv[u] = *(const u32x4*)(base + 16 * min(c0 + 16 * u + s, nch - 1));
+        for (int u = 0; u < kMaskRowChunks; ++u) wv[u] = *(const u32x4*)(base + 16 * min(c0 + 64 * u + s, nch - 1));
 #pragma unroll
         for (int u = 0; u < kMaskRowChunks; ++u) {
-            const int col0 = 8 * (c0 + 16 * u + s) - mis / 2;      // column of the chunk's first entry
+            const int col0 = 8 * (c0 + 64 * u + s) - mis / 2;      // column of the chunk's first entry
             const int elo = max(-col0, 0), ehi = min(n - col0, 8);  // entries [elo, ehi) lie in the row
             const uint32_t valid = ehi > elo ? ((1u << ehi) - 1u) & ~((1u << elo) - 1u) : 0u;
             uint32_t live = 0, nz = 0;
@@ -251,31 +273,37 @@ __device__ __forceinline__ void mask_row_interval(const MaskRowArgs& m, int w, i
             cnt += __builtin_popcount(live);
         }
     }
-    lo = row16_min_i(lo);
-    hi = row16_max_i(hi);
-    cnt = row16_sum_i(cnt);
-    const int nonzero = row16_max_i(nzall != 0 ? 1 : 0);
+    lo = wave_min_dpp(lo);
+    hi = wave_max_dpp(hi);
+    cnt = wave_sum_dpp(cnt);
+    const int nonzero = wave_max_dpp(nzall != 0 ? 1 : 0);
     if (s == 0 && store)
         m.out[w] = hi < lo ? int2{n, -1} : ((nonzero || cnt != hi - lo + 1) ? int2{-2, -2} : int2{lo, hi});
 }
 
-__global__ __launch_bounds__(64) void mask_rows_kernel(MaskRowArgs m) {
-    const int w = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 4);
-    mask_row_interval(m, min(w, m.nrows - 1), (int)(threadIdx.x & 15), w < m.nrows);
+// mask rows [4 bx, 4 bx + 4), one per wavefront
+__device__ __forceinline__ void mask_rows_block(const MaskRowArgs& m, uint32_t bx, int tid) {
+    const int w = (int)bx * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
+    mask_row_interval(m, min(w, m.nrows - 1), tid & 63, w < m.nrows);
 }
 
-// F32 K/V staging and the mask pre-pass in one launch of 256-thread blocks:
-// blocks [0, 2 sb) stage K (the first sb) and V, the rest find the intervals
-// of 16 mask rows each.
+__global__ __launch_bounds__(256) void mask_rows_kernel(MaskRowArgs m) {
+    mask_rows_block(m, blockIdx.x, (int)threadIdx.x);
+}
+
+// The mask pre-pass and F32 K/V staging in one launch of 256-thread blocks:
+// blocks [0, nmb) find the intervals of four mask rows each (first, so that
+// their memory round trip and VALU work overlap the staging stream), blocks
+// [nmb, nmb + 2 sb) stage K (the first sb) and V.
 template <bool NT>
-__global__ __launch_bounds__(256) void prep_kernel(StageArgs sa, uint32_t sb, MaskRowArgs m) {
+__global__ __launch_bounds__(256) void prep_kernel(StageArgs sa, uint32_t sb, uint32_t nmb, MaskRowArgs m) {
     const uint32_t bx = blockIdx.x;
-    if (bx < 2 * sb) {
-        stage_groups<NT>(sa, bx % sb, (int)(bx / sb), threadIdx.x);
+    if (bx < nmb) {
+        mask_rows_block(m, bx, (int)threadIdx.x);
         return;
     }
-    const int w = (int)(bx - 2 * sb) * 16 + (int)(threadIdx.x >> 4);
-    mask_row_interval(m, min(w, m.nrows - 1), (int)(threadIdx.x & 15), w < m.nrows);
+    const uint32_t sx = bx - nmb;
+    stage_groups<NT>(sa, sx % sb, (int)(sx / sb), threadIdx.x);
 }
 
 template <bool QF16, bool C8, int MM>
@@ -939,13 +967,14 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStre
         const int64_t nrows = (int64_t)a.nq * a.hm * a.bm;
         if (nrows > 0x7fffffff - 15) return hipErrorInvalidValue;
         const MaskRowArgs m{a.mask, a.m_nb1, a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows};
+        const uint32_t nmb = (uint32_t)((nrows + 3) / 4);   // four rows per block
         if (sb > 0) {
-            const uint64_t nb = 2ull * sb + (uint64_t)((nrows + 15) / 16);
+            const uint64_t nb = 2ull * sb + nmb;
             if (nb > 0x7fffffffull) return hipErrorInvalidValue;
-            if (snt) hipLaunchKernelGGL(prep_kernel<true>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, m);
-            else hipLaunchKernelGGL(prep_kernel<false>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, m);
+            if (snt) hipLaunchKernelGGL(prep_kernel<true>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, nmb, m);
+            else hipLaunchKernelGGL(prep_kernel<false>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, nmb, m);
         } else {
-            hipLaunchKernelGGL(mask_rows_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(64), 0, st, m);
+            hipLaunchKernelGGL(mask_rows_kernel, dim3(nmb), dim3(256), 0, st, m);
         }
         launch_pp_mm<1>(a, gm, nblk, ni, is_c8, grid, block, st);
     } else {
