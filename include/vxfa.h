@@ -108,9 +108,11 @@ int vxfa_supports(const vxfa_tensor* q, const vxfa_tensor* k,
  * returns after the launches are queued, with no host synchronisation and no
  * allocation. Output is deterministic for equal inputs (fixed split
  * boundaries and merge order). F32 K/V (the reference's own cache,
- * src/voxtral.cpp:1126-1136, and the encoder's K/V, :1581-1605) are rounded
- * to f16 for the QK^T product (as Q is); a decode step reads them in place,
- * a prefill call copies them to f16 in the context's staging area first. */
+ * src/voxtral.cpp:1126-1136, and the encoder's K/V, :1581-1605): a decode
+ * step reads them in place and keeps both products in F32 with Q unrounded,
+ * as ggml's CPU kernel does for F32 K; a prefill call copies them to f16 in
+ * the context's staging area first and rounds Q, K and V to f16 as for f16
+ * K/V. */
 int vxfa_flash_attn_ext(vxfa_ctx* ctx, const vxfa_tensor* q,
                         const vxfa_tensor* k, const vxfa_tensor* v,
                         const vxfa_tensor* mask, vxfa_tensor* dst, float scale,

@@ -882,9 +882,30 @@ def test_graph_capture_then_larger_eager_calls(runner):
 
 # --- F32 K/V: the reference's own cache and encoder K/V --------------------------
 # voxtral.cpp's KV cache is F32 (src/voxtral.cpp:1126-1136) and its encoder's
-# K/V are F32 mul_mat outputs (:1581-1605). ggml keeps Q in F32 for an F32 K;
-# the path rounds K, V (for QK^T) and Q to f16, so these cases are held to the
-# bar against the restatement (F32 dot products) and the exact reference.
+# K/V are F32 mul_mat outputs (:1581-1605). ggml keeps Q in F32 for an F32 K.
+# Decode does the same (F32 QK^T and P.V); prefill rounds K, V and Q to f16
+# (its tiles reach LDS through direct copies of an f16 staging copy). Every
+# case is held to the bar against the restatement (F32 dot products) and the
+# exact reference; decode also to a bar 100 times tighter.
+
+# F32 decode: both products in F32, so the output agrees with the exact
+# reference and with ggml's F32 restatement to F32 rounding, far inside the
+# bar (f16-rounded Q and K leave errors near 1e-3 on these inputs).
+F32_ATOL, F32_RTOL = 2e-5, 1e-4
+
+
+@pytest.mark.parametrize("n_kv,hd,groups,q_f16", [(1024, 128, 4, False), (8192, 128, 4, False), (3000, 64, 2, False),
+                                                  (700, 128, 1, False), (1024, 128, 4, True)])
+def test_f32_cache_decode_keeps_f32_products(runner, n_kv, hd, groups, q_f16):
+    import gpu_util
+    c = cases.decode_case(n_kv, hq=8 * groups, hkv=8, hd=hd, seed=1300 + n_kv + hd, kv_f32=True, q_f16=q_f16)
+    rc, out = runner.run(c)
+    assert rc == 0
+    for tag, ref in (("ggml-fp32", cases.oracle_ggml(c)), ("f64", cases.oracle_f64(c))):
+        m, r, ok = gpu_util.parity(out, ref, F32_ATOL, F32_RTOL, elem_rtol=F32_RTOL)
+        _say(f"    F32 decode n_kv {n_kv} hd {hd} G {groups} vs {tag}: maxabs={m:.3e} rel={r:.3e} "
+             f"elem={gpu_util.elem_rel(out, ref):.3e}")
+        assert ok, (tag, m, r)
 
 @pytest.mark.parametrize("n_kv", [1, 100, 1024, 8192])
 def test_f32_cache_decode(runner, n_kv):

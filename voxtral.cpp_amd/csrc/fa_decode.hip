@@ -6,8 +6,8 @@
 // n_tokens = 1 (step graphs :1959-1962 and :2050-2053), where every KV head
 // serves G = Hq / Hkv query heads (32 / 8 = 4). The cache is f16 (the
 // configured layout) or F32 (the reference's own cache type,
-// src/voxtral.cpp:1126-1136); F32 tiles are rounded to f16 as they are
-// loaded for the QK^T product and used as F32 in the P.V product.
+// src/voxtral.cpp:1126-1136); against F32 K/V both products are F32, as in
+// ggml's CPU kernel for F32 K (Q is not rounded to f16).
 //
 // Two kernels on the caller's stream:
 //   fa_decode         grid (n_split * Hkv, B), kDecodeWaves wavefronts per
@@ -34,10 +34,11 @@
 // Inside a wavefront (tiles of TP positions, 32 for f16 and 16 for F32 K/V,
 // so a tile is 16 KB either way; software pipelined: the next tile's K/V
 // loads are in flight while the current tile is computed):
-//   QK^T  v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims). The A operand
-//         holds the G query heads replicated 16/G times, so every lane gets
-//         the scores of all G heads for one position: no cross-lane dot
-//         reduction.
+//   QK^T  v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims); against F32
+//         K, v_mfma_f32_16x16x4f32 per (16 positions, 4 dims) with F32 Q.
+//         The A operand holds the G query heads replicated 16/G times, so
+//         every lane gets the scores of all G heads for one position: no
+//         cross-lane dot reduction.
 //   K     read like V, D / 8 lanes per row and 16 contiguous bytes per
 //         lane, so one load instruction reads whole 256-byte head rows, then
 //         turned through a wavefront-private LDS tile (rows in, 16-byte chunks
@@ -178,9 +179,11 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
     __shared__ float lds_m[DEC_WAVES][G];
     __shared__ float lds_l[DEC_WAVES][G];
     __shared__ int lds_red[2 * DEC_WAVES];
-    __shared__ half8 lds_q[G * D / 8];   // the group's query heads, f16, [G][D]
+    // the group's query heads [G][D]: f16 against f16 K, F32 against F32 K
+    __shared__ __align__(16) char lds_q_raw[G * D * (KV32 ? 4 : 2)];
     __shared__ float2 lds_rope[D / 2];   // cos / sin of each pair's rotary angle (with rope_pos)
-    __shared__ __align__(16) _Float16 lds_kt[DEC_WAVES * TP * D];   // each wavefront's f16 K tile
+    // each wavefront's K tile: TP rows of f16 (f16 K) or F32 (F32 K), 8 KiB either way
+    __shared__ __align__(16) char lds_kt_raw[DEC_WAVES * TP * D * ESZ];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -278,25 +281,12 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
         uint16_t m[NG][4];
     };
     using Tile = std::conditional_t<KV32, TileF, TileH>;
-    // K entry i as f16 (F32 rounded, as ggml's f16 dot does with Q)
-    auto k8 = [&](const Tile& T, int i) -> half8 {
-        if constexpr (KV32) {
-            half8 r;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                r[e] = (_Float16)T.k[i][0][e];
-                r[4 + e] = (_Float16)T.k[i][1][e];
-            }
-            return r;
-        } else {
-            return T.k[i];
-        }
-    };
     // The wavefront's f16 K tile in LDS: row r, 16-byte chunk c at chunk
     // c ^ f(r) of the row (f(r) = r mod 16 at hd 128, (r / 2) mod 8 at hd 64):
     // the 16 rows one MFMA operand read takes from one column of chunks fall
     // on 16 different bank groups.
-    _Float16* const kt = lds_kt + wave * TP * D;
+    _Float16* const kt = reinterpret_cast<_Float16*>(lds_kt_raw) + wave * TP * D;
+    float* const ktf = reinterpret_cast<float*>(lds_kt_raw) + wave * TP * D;
     auto kt_at = [](int r, int c) { return r * D + 8 * (c ^ ((D == 64 ? (r >> 1) : r) & (NCH - 1))); };
     auto vval = [&](const Tile& T, int i, int j) -> float {
         if constexpr (KV32) return T.v[i][j >> 2][j & 3];
@@ -411,12 +401,11 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
     // the wait for it stays below them.)
     asm volatile("" : "+v"(rope_p) : : "memory");
     if (a.rope_pos && tid < D / 2) lds_rope[tid] = rope_cs_chain<D / 2>(rope_p, tid, a.rope_ts);
+    half8* const lds_q = reinterpret_cast<half8*>(lds_q_raw);
+    float* const lds_qf = reinterpret_cast<float*>(lds_q_raw);
     if (q_loader) {
-        half8 qh8;
-        if constexpr (QF16) {
-            qh8 = __builtin_bit_cast(half8, qraw[0]);
-        } else {
-            float x[8];
+        float x[8];
+        if constexpr (!QF16) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 x[e] = qraw[0][e];
@@ -424,17 +413,47 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
             }
             // rotary embedding of the query (position of batch b's token)
             if (a.rope_pos) rope8_tab(x, 8 * (tid % (D / 8)), lds_rope, a.rope_dims);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qh8[e] = (_Float16)x[e];
         }
-        lds_q[tid] = qh8;
+        if constexpr (KV32) {
+            // F32 K: Q stays F32 (ggml's F32 dot converts Q to F32, exactly)
+            if constexpr (QF16) {
+                const half8 qh = __builtin_bit_cast(half8, qraw[0]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = (float)qh[e];
+            }
+            *(floatx4*)(lds_qf + 8 * tid) = floatx4{x[0], x[1], x[2], x[3]};
+            *(floatx4*)(lds_qf + 8 * tid + 4) = floatx4{x[4], x[5], x[6], x[7]};
+        } else {
+            half8 qh8;
+            if constexpr (QF16) {
+                qh8 = __builtin_bit_cast(half8, qraw[0]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qh8[e] = (_Float16)x[e];
+            }
+            lds_q[tid] = qh8;
+        }
     }
     __syncthreads();
+    // MFMA A operands. f16 K: head (lane & 15) % G, dims 32 ks + 8 (lane / 16)
+    // .. + 7 of step ks. F32 K (v_mfma_f32_16x16x4f32, one dim per lane and
+    // step): lane l takes dim (D / 4) (l / 16) + s at step s, so its D / 4
+    // values of Q (and of each K row) are contiguous.
     half8 qa[KS];
+    float qf[KV32 ? D / 4 : 1];
     {
         const int m = (lane & 15) % G;
+        if constexpr (KV32) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qa[ks] = lds_q[(m * D + 32 * ks + 8 * (lane >> 4)) / 8];
+            for (int cq = 0; cq < D / 16; ++cq) {
+                const floatx4 v = *(const floatx4*)(lds_qf + m * D + (D / 4) * (lane >> 4) + 4 * cq);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qf[4 * cq + e] = v[e];
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qa[ks] = lds_q[(m * D + 32 * ks + 8 * (lane >> 4)) / 8];
+        }
     }
 
     float m_run[4], l_run[4];
@@ -452,22 +471,49 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
         // instructions of one wavefront execute in order, so its reads see
         // its writes; the previous tile's reads have returned (its MFMAs used
         // them) before these writes issue.
-#pragma unroll
-        for (int i = 0; i < NV; ++i) *(half8*)(kt + kt_at(vrow + i * RPI, lane % CH)) = k8(T, i);
-        __builtin_amdgcn_wave_barrier();
-        half8 kop[NG][KS];
-#pragma unroll
-        for (int grp = 0; grp < NG; ++grp)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                kop[grp][ks] = *(const half8*)(kt + kt_at(16 * grp + (lane & 15), 4 * ks + (lane >> 4)));
         floatx4 sc[NG];
+        if constexpr (KV32) {
+            // F32 rows, 16-byte chunk c of row r at chunk c ^ (r % 16): the 16
+            // rows of one operand read (one chunk each) fall on 16 bank groups.
+            // S^T in F32: v_mfma_f32_16x16x4f32, D / 4 steps, the products and
+            // their sums in F32 as ggml's F32 dot (the matrix pipe has time to
+            // spare in an HBM-bound kernel).
 #pragma unroll
-        for (int grp = 0; grp < NG; ++grp) {
-            sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < NV; ++i) {
+                const int r = vrow + i * RPI, c0 = 2 * (lane % CH);
+                *(floatx4*)(ktf + r * D + 4 * (c0 ^ (r & 15))) = T.k[i][0];
+                *(floatx4*)(ktf + r * D + 4 * ((c0 + 1) ^ (r & 15))) = T.k[i][1];
+            }
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kop[grp][ks], sc[grp], 0, 0, 0);
+            for (int grp = 0; grp < NG; ++grp) {
+                const int r = 16 * grp + (lane & 15);
+                sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int cq = 0; cq < D / 16; ++cq) {
+                    const floatx4 kv = *(const floatx4*)(ktf + r * D + 4 * (((D / 16) * (lane >> 4) + cq) ^ (r & 15)));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        sc[grp] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * cq + e], kv[e], sc[grp], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) *(half8*)(kt + kt_at(vrow + i * RPI, lane % CH)) = T.k[i];
+            __builtin_amdgcn_wave_barrier();
+            half8 kop[NG][KS];
+#pragma unroll
+            for (int grp = 0; grp < NG; ++grp)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    kop[grp][ks] = *(const half8*)(kt + kt_at(16 * grp + (lane & 15), 4 * ks + (lane >> 4)));
+#pragma unroll
+            for (int grp = 0; grp < NG; ++grp) {
+                sc[grp] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    sc[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kop[grp][ks], sc[grp], 0, 0, 0);
+            }
         }
         // scores in log2 units; lane holds head (i % G) at position p0 + 16*grp + (lane & 15)
         float x[NG][4];
