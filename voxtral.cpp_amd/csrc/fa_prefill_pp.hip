@@ -694,29 +694,16 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
         // every P of later blocks stays below 2^TAU unless a new larger score
         // arrives, which the same test catches.
         // The basic block of each half (closed by that branch) holds its 8 MFMAs
-        // and the softmax's fast path; HALF (1 or 2) lays them out: in H1 the 4
-        // K operand reads first, then softmax VALU work while they land, then one
-        // MFMA per 5 VALU instructions; in H2 (operands in registers) one MFMA per
-        // 6 from the start.
-        auto softmax_spec = [&](auto half_tag, const floatx16& sc, float& m, float& l, floatx16 (&o)[DB],
-                                half8 (&p)[2], bool real) {
-            constexpr int HALF = decltype(half_tag)::value;
+        // and the softmax's fast path, which the compiler's max-ILP scheduler
+        // interleaves (the file is built with it). Under the default scheduler
+        // the kernel pinned the order with scheduling groups (in H1 the 4 K
+        // operand reads, then 12 VALU instructions, then one MFMA per 5 VALU;
+        // in H2 one MFMA per 6); with max-ILP those groups measured slower
+        // (encoder layer 21.05 against 20.61 us, realtime encoder implicit
+        // 27.35 against 26.94, alternating A/B on one box).
+        auto softmax_spec = [&](const floatx16& sc, float& m, float& l, floatx16 (&o)[DB], half8 (&p)[2],
+                                bool real) {
             float ls = exps(sc, m, p);
-            if constexpr (HALF == 1) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS reads
-                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);   // VALU
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // VALU
-                }
-            } else if constexpr (HALF == 2) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-                }
-            }
             // 2^TAU (also true for inf / NaN); with a mask, also a row that has
             // no live score yet (its P above were taken against m = 0)
             bool slow = !(ls <= 256.0f);
@@ -788,14 +775,14 @@ __global__ __launch_bounds__(pp::NT) void fa_prefill64_pp(AttnArgs a, GridMap gm
             // operands are in registers while K_{t+1} lands.
             pv_mfma(oa, pa, vr);
             s_mfma(sa, qa, kr);
-            softmax_spec(std::integral_constant<int, 1>{}, sb, mb, lb, ob, pb, real_b);
+            softmax_spec(sb, mb, lb, ob, pb, real_b);
             if ((t == 0 ? NS - 1 : t + NS) < ng) issue(t == 0 ? NS - 1 : t + NS);
             // H2: PV_B(t), S_B(t+1); softmax of S_A(t+1)
             mask_fix(sa, t + 1, 0);
             pv_mfma(ob, pb, vr);
             read_v(t + 1, vr);   // V_{t+1}: its block is visible since the previous barrier
             s_mfma(sb, qb, kr);
-            softmax_spec(std::integral_constant<int, 2>{}, sa, ma, la, oa, pa, real_a);
+            softmax_spec(sa, ma, la, oa, pa, real_a);
             // blocks issued so far: up to NS - 1 (t = 0), t + NS (t >= 1)
             const int last = min(t >= 1 ? t + NS : NS - 1, ng - 1);
             wait_blocks_loop<NLD>(last - (t + 2));   // 2 at most: last <= t + NS
