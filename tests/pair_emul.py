@@ -64,7 +64,7 @@ class Shape:
     hkv: int = 8
     b: int = 1
     bk: int = 1
-    mode: str = "tensor"          # "tensor" or "implicit"
+    mode: str = "tensor"          # "tensor", "intervals" (tensor, classes from the pre-pass) or "implicit"
     offset: int = 0               # implicit mask: row i attends j <= i + offset
     window: int = 0               #   and j >= i + offset - window + 1 when window > 0
     m_nb1: int = 0                # mask row stride in bytes (default 2 n_kv: unpadded rows)
@@ -88,7 +88,7 @@ class Shape:
         self.k_nb3 = self.k_nb1 * self.kv_rows
         self.m_nb2 = self.m_nb1 * self.nq
         self.m_nb3 = self.m_nb2 * self.hm
-        if self.mode == "tensor" and self.mask is None:
+        if self.mode != "implicit" and self.mask is None:
             i = np.arange(self.nq)[:, None]
             j = np.arange(self.nkv)[None, :]
             causal = np.where(j <= i + self.offset, 0, NEG_INF).astype(np.uint16)
@@ -146,6 +146,28 @@ def mask_words_expected(sh: Shape, mplane_entry, T, j):
                     else:
                         bits = int(mplane_entry(row, kv))
                     word |= bits << (16 * e)
+                out[lane, kvb, w] = word
+    return out
+
+
+def mask_words_interval(sh: Shape, table, T, j, plant=None):
+    """The kernel's mw_interval (MM = 3, a tile whose rows are all intervals):
+    lane (nl, hh) forms its words from row 32 T + nl's interval {lo, hi}
+    (row min(., n_q - 1) for rows past n_q): 0 where lo <= kv <= hi and
+    kv < n_kv, -inf elsewhere."""
+    out = np.zeros((64, 2, 8), dtype=np.uint32)
+    for lane in range(64):
+        nl, hh = lane & 31, lane >> 5
+        lo, hi = table[min(32 * T + nl, sh.nq - 1)]
+        if plant == "interval_words_hi_open":
+            hi += 1
+        for kvb in range(2):
+            for w in range(8):
+                word = 0
+                for e in range(2):
+                    kv = TK * j + 32 * kvb + int(pf_kv_of(hh, 2 * w + e))
+                    live = kv < sh.nkv and lo <= kv <= hi
+                    word |= (0 if live else NEG_INF) << (16 * e)
                 out[lane, kvb, w] = word
     return out
 
@@ -248,6 +270,47 @@ def classify_kernel(sh: Shape, buf, plane_off, T, j, plant=None):
     return 3 if (nonzero or TK * j + TK > sh.nkv) else 1
 
 
+_TABLES = {}   # the pre-pass table of each (shape, plane), made once
+
+
+def interval_table(sh: Shape, bb, h):
+    """The mask pre-pass's table for the rows of plane (h % hm, bb % bm)
+    (dma_emul.mask_row_interval of each row at its 16-byte alignment)."""
+    from dma_emul import mask_row_interval
+    out = []
+    for i in range(sh.nq):
+        off = sh.m_mis + (bb % sh.bm) * sh.m_nb3 + (h % sh.hm) * sh.m_nb2 + i * sh.m_nb1
+        out.append(mask_row_interval(sh.mask[bb % sh.bm, h % sh.hm, i], off % 16))
+    return out
+
+
+def classify_intervals(sh: Shape, table, tA, tB, hasA, nk, plant=None):
+    """The kernel's MM = 3 block classes, from the rows' intervals: per block
+    j < nk of tile T, live when a real row's interval meets [64 j, 64 j + 64)
+    (within n_kv) or a real row is not an interval (-2), all-zero when every
+    real row's interval holds the block and the block lies within n_kv,
+    mixed otherwise; rows past n_q take no part. Tile A only when it exists."""
+    cls = {}
+    for s_, T in ((0, tA), (1, tB)):
+        if s_ == 0 and not hasA:
+            continue
+        for j in range(nk):
+            c0, c1 = TK * j, min(TK * j + TK, sh.nkv) - 1
+            live, cov = False, True
+            for r in range(32):
+                row = 32 * T + r
+                if row >= sh.nq:
+                    continue
+                lo, hi = table[row]
+                meets = lo <= c1 and hi >= c0
+                holds = lo <= c0 and (hi >= c1 or plant == "holds_ignores_hi") and lo >= 0
+                live = live or (lo == -2 and plant != "non_interval_dead") or meets
+                cov = cov and lo != -2 and holds
+            full = cov and TK * j + TK <= sh.nkv
+            cls[(s_, j)] = 0 if not live else (1 if full else 3)
+    return cls
+
+
 def classify(words):
     live = np.any(words != 0xFC00FC00)
     nonzero = np.any((words & 0x7FFF7FFF) != 0)
@@ -289,7 +352,7 @@ def emulate_pair(sh: Shape, heads=None, batches=None, plant=None):
     np_ = (nt + 1) // 2
     heads = heads if heads is not None else sorted({0, sh.hq - 1})
     batches = batches if batches is not None else sorted({0, sh.b - 1})
-    buf = sh.mask_buffer() if sh.mode == "tensor" else None
+    buf = sh.mask_buffer() if sh.mode != "implicit" else None
     n_blocks = 0
     for bb in batches:
         for h in heads:
@@ -344,6 +407,27 @@ def _emulate_wg(sh, p, h, bb, hk, bkv, nt, nk, buf, stored, plant):
             zero = all(v in (0, 0x8000) for v in vals) and TK * j + TK <= sh.nkv
             want = 0 if not live else (1 if zero else 3)
             _check(c == want, f"class of ({T}, {j}): {c}, entries give {want}")
+    elif sh.mode == "intervals":
+        key = (bb % sh.bm, h % sh.hm)
+        if key not in _TABLES.get(id(sh), {}):
+            _TABLES.setdefault(id(sh), {})[key] = interval_table(sh, bb, h)
+        tab = _TABLES[id(sh)][key]
+        cls = classify_intervals(sh, tab, tA, tB, hasA, nk, plant)
+        for (s_, j), c in cls.items():
+            T = tB if s_ else tA
+            rows = range(32 * T, min(32 * T + 32, sh.nq))
+            vals = [int(sh.mask[bb % sh.bm, h % sh.hm, r, k]) for r in rows for k in range(TK * j, TK * j + TK)
+                    if k < sh.nkv]
+            live = any(v != NEG_INF for v in vals)
+            zero = all(v in (0, 0x8000) for v in vals) and TK * j + TK <= sh.nkv
+            want = 0 if not live else (1 if zero else 3)
+            # sound for any mask: every block with a live entry computed, the
+            # mask skipped only where every entry is 0
+            _check(not (want and not c), f"block ({T}, {j}) with live entries classed dead")
+            _check(not (c == 1 and want != 1), f"block ({T}, {j}) classed all-zero, entries give {want}")
+            # exact when the tile's rows are intervals (or empty)
+            if all(tab[r][0] != -2 for r in rows):
+                _check(c == want, f"class of ({T}, {j}) from intervals: {c}, entries give {want}")
     else:
         for j in range(nk):
             cls[(1, j)] = cls_formula(sh, tB, j)
@@ -368,13 +452,23 @@ def _emulate_wg(sh, p, h, bb, hk, bkv, nt, nk, buf, stored, plant):
             j = live[iT + k * wT]
             key = (T, j)
             computed[key] = computed.get(key, 0) + 1
-    if sh.mode == "tensor":
+    if sh.mode != "implicit":
         ent = lambda row, pos: sh.mask[bb % sh.bm, h % sh.hm, row, pos]
         for (T, j) in computed:
             if cls[(1 if T == tB else 0, j)] == 3:
-                words = mask_words_kernel(sh, buf, plane_off, T, j, plant)
-                _check(words == mask_words_expected(sh, ent, T, j),
-                       f"mask words of block ({T}, {j}) differ from the entries")
+                rows = range(32 * T, min(32 * T + 32, sh.nq))
+                if sh.mode == "intervals" and all(tab[r][0] != -2 for r in rows):
+                    # words from the intervals; rows past n_q are not stored
+                    words = mask_words_interval(sh, tab, T, j, plant)
+                    want = mask_words_expected(sh, ent, T, j)
+                    real = np.array([32 * T + (ln & 31) < sh.nq for ln in range(64)])
+                    # +0 and -0 both read as zero (the tensor may hold either)
+                    _check(((words[real] & 0x7FFF7FFF) == (want[real] & 0x7FFF7FFF)).all(),
+                           f"interval words of block ({T}, {j}) differ from the entries")
+                else:
+                    words = mask_words_kernel(sh, buf, plane_off, T, j, plant)
+                    _check(words == mask_words_expected(sh, ent, T, j),
+                           f"mask words of block ({T}, {j}) differ from the entries")
     want = {(tB, j) for j in liveB} | {(tA, j) for j in liveA}
     _check(set(computed) == want and all(v == 1 for v in computed.values()),
            f"blocks computed {sorted(computed.items())} != live {sorted(want)}")

@@ -19,6 +19,7 @@ hipError_t launch_decode(const AttnArgs&, int, int, hipStream_t) { return hipErr
 hipError_t launch_prefill(const AttnArgs&, int, int, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_prefill64_pp(const AttnArgs&, const StageReq*, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_prefill_pair(const AttnArgs&, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_mask_prep(const AttnArgs&, const StageReq*, hipStream_t) { return hipErrorInvalidValue; }
 bool prefill_pair_fits(const AttnArgs&) { return true; }
 hipError_t launch_zero(float*, int64_t, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_kv_append(const AppendArgs&, hipStream_t) { return hipErrorInvalidValue; }

@@ -123,20 +123,33 @@ hipError_t launch_prefill(const AttnArgs& a, int, int, hipStream_t) {
     common(a);
     return hipSuccess;
 }
+void check_mask_table(const AttnArgs& a) {
+    const size_t bytes = (size_t)a.nq * a.hm * a.bm * 8;
+    if (!a.mask_rows || !inside_one(a.mask_rows, bytes)) fail("mask interval table outside the workspace");
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(a.mask_rows);
+    if (g_stage_hi > g_stage_lo && lo < g_stage_hi && g_stage_lo < lo + bytes)
+        fail("mask interval table overlaps the staged K/V");
+}
+hipError_t launch_mask_prep(const AttnArgs& a, const StageReq* stage, hipStream_t) {
+    ++g_launches;
+    if (stage) check_stage(*stage);
+    if (!a.mask) fail("mask pre-pass without a mask");
+    check_mask_table(a);
+    return hipSuccess;
+}
 hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStream_t) {
     if (stage) check_stage(*stage);
     common(a);
-    if (a.mask) {
-        const size_t bytes = (size_t)a.nq * a.hm * a.bm * 8;
-        if (!a.mask_rows || !inside_one(a.mask_rows, bytes)) fail("mask interval table outside the workspace");
-        const uintptr_t lo = reinterpret_cast<uintptr_t>(a.mask_rows);
-        if (g_stage_hi > g_stage_lo && lo < g_stage_hi && g_stage_lo < lo + bytes)
-            fail("mask interval table overlaps the staged K/V");
-    }
+    if (a.mask) check_mask_table(a);
     return hipSuccess;
 }
 hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t) {
     common(a);
+    if (a.mask_rows) {
+        // the interval table is only read after the pre-pass that fills it
+        if (!a.mask) fail("interval table without a mask");
+        check_mask_table(a);
+    }
     return hipSuccess;
 }
 bool prefill_pair_fits(const AttnArgs&) { return true; }

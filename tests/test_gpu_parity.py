@@ -935,6 +935,91 @@ def test_f32_decoder_prefill_439_causal(runner):
     check_case(runner, cases.prefill_case(439, seed=1207, kv_f32=True))
 
 
+def _runner_with_env(**kw):
+    """A second context created with tuning variables set (a context reads
+    them once, at creation)."""
+    import os
+    import gpu_util
+    old = {k: os.environ.get(k) for k in kw}
+    os.environ.update({k: str(v) for k, v in kw.items()})
+    try:
+        return gpu_util.Runner()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+# F32 K/V with a mask tensor on the short masked prefill (voxtral's decoder
+# prefill as the unchanged application calls it): the staging launch also
+# finds each mask row's live interval and the kernel takes its block classes
+# from them instead of reading the mask first; mixed blocks still read their
+# words from the tensor.
+
+@pytest.mark.parametrize("n,nkv", [(339, 439), (439, 439), (64, 65), (129, 511), (2, 130)])
+def test_f32_prefill_interval_classes_bitwise(runner, n, nkv):
+    """Causal masks (rows are intervals): the same bits as classifying from
+    the mask (VXFA_PAIR_INTERVALS=0 on a second context), within the bar of
+    the oracle."""
+    c = cases.prefill_case(n, seed=1400 + n + nkv, kv_offset=nkv - n, kv_f32=True)
+    out = check_case(runner, c)
+    other = _runner_with_env(VXFA_PAIR_INTERVALS=0)
+    try:
+        rc, out2 = other.run(c)
+        assert rc == 0
+    finally:
+        other.close()
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["sparse", "bias", "empty_rows", "window"])
+def test_f32_prefill_masks_through_intervals(runner, kind):
+    """Masks whose rows are not all intervals take the fallback (every block
+    of such a row's tile computed with its words from the tensor): isolated
+    live entries at chunk and tile edges, finite additive values, fully masked
+    rows, and a sliding window as a tensor; F32 K/V, against the oracle."""
+    rng = np.random.default_rng(1500 + len(kind))
+    if kind == "sparse":
+        n, nkv = 71, 133
+        c = cases.prefill_case(n, causal=False, kv_offset=nkv - n, seed=1501, kv_f32=True)
+        c = cases.with_mask(c, _sparse_mask(rng, n, nkv))
+    elif kind == "bias":
+        c = cases.prefill_case(90, hq=8, hkv=2, seed=1502, kv_f32=True)
+        m = c.bufs["mask"].reshape(90, 90)
+        bias = cases.f16_bits(rng.uniform(-3, 3, size=m.shape).astype(np.float32))
+        c.bufs["mask"] = np.where(m == cases.NEG_INF_F16, m, bias).astype(np.uint16)
+    elif kind == "empty_rows":
+        c = cases.prefill_case(70, hq=4, hkv=2, seed=1503, kv_f32=True)
+        m = c.bufs["mask"].reshape(70, 70)
+        m[5, :] = cases.NEG_INF_F16
+        m[69, :] = cases.NEG_INF_F16
+    else:
+        n, nkv = 200, 437
+        c = cases.prefill_case(n, causal=False, kv_offset=nkv - n, seed=1504, kv_f32=True)
+        c = cases.with_mask(c, cases.implicit_mask(n, nkv, nkv - n, 50))
+    if kind == "sparse":
+        # A few live entries per row: each output follows a handful of V rows,
+        # and the f16 rounding of Q that prefill applies against F32 K (ggml
+        # keeps Q in F32 there) shows at up to ~1.3x the max-abs bar on this
+        # mask. Held to the bar against the exact reference with Q rounded as
+        # the kernel does, and to twice the bar against ggml's F32 semantics.
+        import gpu_util
+        rc, out = runner.run(c)
+        assert rc == 0
+        m1, r1, ok1 = gpu_util.parity(out, cases.oracle_f64(c, q_f16=True), ATOL, RTOL)
+        m2, r2, ok2 = gpu_util.parity(out, cases.oracle_f64(c), 2 * ATOL, RTOL)
+        _say(f"    sparse F32 prefill: vs exact with Q rounded maxabs={m1:.3e} rel={r1:.3e}; "
+             f"vs exact F32 Q maxabs={m2:.3e} rel={r2:.3e}")
+        assert ok1, (m1, r1)
+        assert ok2, (m2, r2)
+        return
+    out = check_case(runner, c)
+    if kind == "empty_rows":
+        assert (out[0, 5] == 0).all() and (out[0, 69] == 0).all()
+
+
 def test_f32_prefill_beyond_staging_reports_no_workspace(runner):
     """K and V of 16384 rows x 8 x 128 need 64 MiB of f16 staging; the context
     holds 32 MiB, so the call returns VXFA_NO_WORKSPACE and launches nothing."""

@@ -41,6 +41,14 @@ SHAPES = [
     Shape(130, 257, mask=_random_mask(130, 257, 1)),
     Shape(96, 500, hq=4, hkv=2, b=3, bk=3, hm=2, bm=3, m_mis=4, mask=_random_mask(96, 500, 2, hm=2, bm=3)),
     Shape(77, 77, hq=8, hkv=1, b=2, bk=1, m_nb1=256),       # padded rows, GQA 8, kv batch broadcast
+    # classes from the mask pre-pass's intervals (F32 K/V staged in the same launch)
+    Shape(339, 439, offset=100, mode="intervals"),          # voxtral's decoder prefill after 100 cached rows
+    Shape(439, 439, m_mis=2, mode="intervals"),
+    Shape(300, 300, mode="intervals", mask=_window_mask(300, 300, 0, 100)),
+    Shape(130, 257, mode="intervals", mask=_random_mask(130, 257, 3)),   # holes and finite values: fallback
+    Shape(96, 500, hq=4, hkv=2, b=3, bk=3, hm=2, bm=3, m_mis=4, mode="intervals",
+          mask=_random_mask(96, 500, 4, hm=2, bm=3)),
+    Shape(65, 65, m_mis=6, mode="intervals"),
 ]
 
 
@@ -75,3 +83,15 @@ def test_at_most_two_blocks_per_wavefront():
 def test_pair_emulation_catches_planted_mistakes(plant):
     with pytest.raises(Violation):
         emulate_pair(Shape(439, 439), plant=plant)
+
+
+@pytest.mark.parametrize("plant", ["holds_ignores_hi", "non_interval_dead", "interval_words_hi_open"])
+def test_interval_classes_catch_planted_mistakes(plant):
+    """The pre-pass route: a block counted as wholly covered by an interval
+    that ends inside it, a non-interval row's blocks left dead, or mask words
+    formed with an interval one entry too long each fail the check against
+    the entries."""
+    sh = Shape(339, 439, offset=100, mode="intervals") if plant != "non_interval_dead" else \
+        Shape(130, 257, mode="intervals", mask=_random_mask(130, 257, 3))
+    with pytest.raises(Violation):
+        emulate_pair(sh, plant=plant)

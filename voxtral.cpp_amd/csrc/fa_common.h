@@ -63,10 +63,11 @@ struct AttnArgs {
     const float* k_new;
     const float* v_new;
     int64_t kn_nb3, vn_nb3;
-    // hd 64 prefill with a mask tensor: per mask row (batch bm_i, plane p,
-    // row q at (bm_i * hm + p) * nq + q) the live interval {lo, hi} when the
-    // row is 0 on [lo, hi] and -inf elsewhere ({n_kv, -1}: no live entry),
-    // else {-2, -2}; written by a pre-pass launch into workspace scratch
+    // prefill with a mask tensor (the hd 64 pipelined kernel; the short masked
+    // prefill after F32 staging): per mask row (batch bm_i, plane p, row q at
+    // (bm_i * hm + p) * nq + q) the live interval {lo, hi} when the row is 0
+    // on [lo, hi] and -inf elsewhere ({n_kv, -1}: no live entry), else
+    // {-2, -2}; written by a pre-pass launch into workspace scratch
     int2* mask_rows;
 };
 
@@ -580,8 +581,13 @@ hipError_t launch_prefill(const AttnArgs& a, int head_dim, int waves, hipStream_
 // copies), or null; with a mask tensor the conversion and the pre-pass share
 // one launch
 hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStream_t stream);
+// the mask pre-pass: the live interval of each of the nq * hm * bm rows of
+// a.mask into a.mask_rows, in one launch with the F32 -> f16 staging of
+// *stage when stage is not null
+hipError_t launch_mask_prep(const AttnArgs& a, const StageReq* stage, hipStream_t stream);
 // masked hd 128 prefill with n_kv <= 512 (a mask tensor or an implicit mask;
-// a rotary embedding of F32 Q)
+// a rotary embedding of F32 Q); with a mask tensor and a.mask_rows set the
+// intervals there (launch_mask_prep first) give the block classes
 hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t stream);
 // whether launch_prefill_pair takes these strides (its 32-bit offsets)
 bool prefill_pair_fits(const AttnArgs& a);

@@ -22,7 +22,10 @@
 //   or mixed (mask values added). With an implicit mask they follow from the
 //   formula; with a mask tensor each wavefront first reads the mask of two
 //   candidate blocks, (B, w) and (A, 7 - w), as whole row segments, and
-//   classifies them.
+//   classifies them; with a mask tensor whose rows' live intervals a pre-pass
+//   has found (MM 3: the launch that stages F32 K/V runs it) they follow
+//   from the intervals, and a tile whose rows are all intervals also forms
+//   its mixed blocks' mask words from them.
 //   Assignment: B's live blocks go to wavefronts 0 .. wB - 1, A's to the rest
 //   in reverse order (wB in proportion to the live counts), so under a causal
 //   mask each wavefront computes the block it classified. With at most 8 live KV tiles per query tile
@@ -70,11 +73,14 @@ __device__ __forceinline__ void pr_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int MM, bool QF16>   // MM 1: mask tensor, 2: implicit mask
+// MM 1: mask tensor, 2: implicit mask, 3: mask tensor with the live interval
+// of each mask row found by a pre-pass (a.mask_rows; see mask_rows_kernel)
+template <int MM, bool QF16>
 __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm, DivMod hmd, DivMod bmd, int nt,
                                                            int nk) {
     using namespace pr;
-    static_assert(MM == 1 || MM == 2, "masked calls only");
+    static_assert(MM == 1 || MM == 2 || MM == 3, "masked calls only");
+    constexpr bool TENSOR = MM == 1 || MM == 3;   // mixed blocks read their mask words from the tensor
     __shared__ __attribute__((aligned(16))) char sV[MAXK * VT];   // V tiles; then the published O
     __shared__ __attribute__((aligned(16))) char sQ[2 * QT];      // query tiles A (slot 0), B (slot 1)
     __shared__ float s_ml[2 * NW * 64];                           // published m, then l
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     // n_q * m_nb1 below 2^31 and m_nb1 below 2^24). Rows past n_q read the
     // tile's first row (their entries are dropped).
     const char* mplane = nullptr;
-    if constexpr (MM == 1)
+    if constexpr (TENSOR)
         mplane = (const char*)a.mask + (int64_t)hmd.mod((uint32_t)h) * a.m_nb2 + (int64_t)bmd.mod((uint32_t)b) * a.m_nb3;
     const uint32_t mnb = (uint32_t)a.m_nb1;
     const uint32_t rowbytes = 2u * (uint32_t)a.nkv;   // bytes of mask data per row
@@ -196,6 +202,22 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
                 mw[kvb][w] = pair;
             }
     };
+    // MM 3, from the row's interval {lo, hi} ({n_kv, -1}: no live entry)
+    auto mw_interval = [&](int j, int2 ivl, uint32_t (&mw)[2][8]) {
+#pragma unroll
+        for (int kvb = 0; kvb < 2; ++kvb)
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                uint32_t pair = 0;
+#pragma unroll
+                for (int e2 = 0; e2 < 2; ++e2) {
+                    const int kv = TK * j + 32 * kvb + pf_kv_of(hh, 2 * w + e2);
+                    const bool live = kv < a.nkv && kv >= ivl.x && kv <= ivl.y;
+                    pair |= (live ? 0u : (uint32_t)kF16NegInf) << (16 * e2);
+                }
+                mw[kvb][w] = pair;
+            }
+    };
     // class of block (T, j) from the formula: 0 dead, 1 every entry 0, 3 mixed
     // (a KV tile running past n_kv is mixed)
     auto cls_formula = [&](int T, int j) -> int {
@@ -242,6 +264,8 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     const int jB = wave, jA = MAXK - 1 - wave;
     const bool candB = jB < nk, candA = hasA && jA < nk;
     uint32_t liveA = 0, liveB = 0, mixA = 0, mixB = 0;
+    int2 iv = {0, 0};                       // MM 3: the interval of row 32 T + (lane % 32), T = A / B by lane half
+    bool ivA = false, ivB = false;          // MM 3: every real row of tile A / B is an interval (or empty)
     if constexpr (MM == 1) {
         // A candidate's 32 rows are read as the 16-byte-aligned chunks that
         // cover each row's 128-byte segment: nine lanes per row (lane 63
@@ -297,13 +321,56 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
             if (candA) s_cls[jA] = (uint8_t)cA;
         }
         pr_lds_barrier();
+    } else if constexpr (MM == 3) {
+        // Classes from the rows' intervals, with no mask reads and no barrier:
+        // lane l holds row 32 T + (l % 32) of tile T = A (l < 32) or B. Per
+        // block j (positions [64 j, 64 j + 64) within n_kv) a row is live when
+        // its interval meets the block and covers it when it holds all of it;
+        // a row that is not an interval makes every block of its tile live and
+        // mixed (its words then come from the tensor, correct for any mask),
+        // an empty row makes none live and none covered, a row past n_q (or of
+        // a missing tile A) counts as covering and not live. Ballots over each
+        // half of the wavefront give the tile's live and mixed blocks.
+        const int2* tab = a.mask_rows + ((int64_t)bmd.mod((uint32_t)b) * a.hm + hmd.mod((uint32_t)h)) * a.nq;
+        const int Tl = lane < 32 ? tA : tB;
+        const int rowl = 32 * Tl + nl;
+        iv = tab[min(rowl, a.nq - 1)];   // unconditional: no wait at a join
+        issue_q();   // after the interval load: its wait does not include Q's
+        const bool realrow = rowl < a.nq && (lane >= 32 || hasA);
+        const uint64_t bad = __ballot(realrow && iv.x == -2);
+        ivA = (uint32_t)bad == 0u;
+        ivB = (uint32_t)(bad >> 32) == 0u;
+        uint32_t lv = 0, cv = 0;
+#pragma unroll
+        for (int j = 0; j < MAXK; ++j) {
+            const int c0 = TK * j, c1 = min(TK * j + TK, a.nkv) - 1;
+            const bool inb = j < nk;
+            const bool meets = iv.x <= c1 && iv.y >= c0;       // false for an empty row {n, -1}
+            const bool holds = iv.x <= c0 && iv.y >= c1 && iv.x >= 0;
+            const bool live = inb && (iv.x == -2 || meets);
+            const bool cov = iv.x != -2 && holds;
+            lv |= (realrow && live ? 1u : 0u) << j;
+            cv |= (!realrow || cov ? 1u : 0u) << j;
+        }
+#pragma unroll
+        for (int j = 0; j < MAXK; ++j) {
+            const uint64_t bl = __ballot((lv >> j) & 1u), bc = __ballot(!((cv >> j) & 1u));
+            const uint32_t la = (uint32_t)bl != 0u, lb = (uint32_t)(bl >> 32) != 0u;
+            // a KV tile running past n_kv is mixed (its positions there are -inf)
+            const uint32_t fa = (uint32_t)bc == 0u && TK * j + TK <= a.nkv;
+            const uint32_t fb = (uint32_t)(bc >> 32) == 0u && TK * j + TK <= a.nkv;
+            liveA |= la << j;
+            liveB |= lb << j;
+            mixA |= (la & (fa ^ 1u)) << j;
+            mixB |= (lb & (fb ^ 1u)) << j;
+        }
     } else {
         issue_q();
     }
     // Lane L < 16 takes block (A, L) or (B, L - 8) and two ballots form the
     // masks (a loop over the blocks in every wavefront compiled to ~500
     // dependent scalar and branch instructions: 1.7 us).
-    {
+    if constexpr (MM != 3) {
         const int lc = lane & 15;
         const int jl = lc & (MAXK - 1);
         const bool onb = lc >= MAXK;
@@ -350,12 +417,26 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
     const bool mix1 = nblk > 1 && ((mix >> j1) & 1u);
     uint32_t mw0[2][8], mw1[2][8];
     u32x4 chr0[2][3], chr1[2][3];
+    // MM 3: a tile whose rows are all intervals forms its mixed blocks' words
+    // from the lane's row interval (the row's lane in the classification
+    // layout is nl for tile A, 32 + nl for tile B); any other tile reads them
+    // from the tensor
+    bool mw_tensor = TENSOR;
+    int2 ivr = {0, 0};
+    if constexpr (MM == 3) {
+        mw_tensor = !(onB ? ivB : ivA);
+        const int src = (onB ? 32 : 0) + nl;
+        ivr.x = __shfl(iv.x, src, 64);
+        ivr.y = __shfl(iv.y, src, 64);
+    }
     if (mix0) {
-        if constexpr (MM == 1) mw_issue(T, j0, chr0);
+        if (mw_tensor) mw_issue(T, j0, chr0);
+        else if constexpr (MM == 3) mw_interval(j0, ivr, mw0);
         else mw_formula(T, j0, mw0);
     }
     if (mix1) {
-        if constexpr (MM == 1) mw_issue(T, j1, chr1);
+        if (mw_tensor) mw_issue(T, j1, chr1);
+        else if constexpr (MM == 3) mw_interval(j1, ivr, mw1);
         else mw_formula(T, j1, mw1);
     }
 
@@ -391,7 +472,7 @@ __global__ __launch_bounds__(pr::NT) void fa_prefill_pair(AttnArgs a, GridMap gm
 
     // ---- Q: wait for every load, round to f16, stage -------------------------
     wait_all_mem();
-    if constexpr (MM == 1) {
+    if (mw_tensor) {
         if (mix0) mw_finish(T, j0, chr0, mw0);
         if (mix1) mw_finish(T, j1, chr1, mw1);
     }
@@ -671,6 +752,9 @@ hipError_t launch_prefill_pair(const AttnArgs& a, hipStream_t st) {
     if (a.im_causal) {
         if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<2, true>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
         else hipLaunchKernelGGL((fa_prefill_pair<2, false>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
+    } else if (a.mask_rows) {
+        if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<3, true>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
+        else hipLaunchKernelGGL((fa_prefill_pair<3, false>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
     } else {
         if (a.q_f16) hipLaunchKernelGGL((fa_prefill_pair<1, true>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);
         else hipLaunchKernelGGL((fa_prefill_pair<1, false>), grid, block, 0, st, a, gm, hmd, bmd, nt, nk);

@@ -930,6 +930,27 @@ static void launch_pp_mm(const AttnArgs& a, const GridMap& gm, int nblk, int ni,
     }
 }
 
+hipError_t launch_mask_prep(const AttnArgs& a, const StageReq* stage, hipStream_t st) {
+    if (!a.mask || !a.mask_rows) return hipErrorInvalidValue;
+    StageArgs sa;
+    uint32_t sb = 0;
+    bool snt = false;
+    if (stage && !make_stage_args(*stage, sa, sb, snt)) return hipErrorInvalidValue;
+    const int64_t nrows = (int64_t)a.nq * a.hm * a.bm;
+    if (nrows <= 0 || nrows > 0x7fffffff - 15) return hipErrorInvalidValue;
+    const MaskRowArgs m{a.mask, a.m_nb1, a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows};
+    const uint32_t nmb = (uint32_t)((nrows + 3) / 4);   // four rows per block
+    if (sb > 0) {
+        const uint64_t nb = 2ull * sb + nmb;
+        if (nb > 0x7fffffffull) return hipErrorInvalidValue;
+        if (snt) hipLaunchKernelGGL(prep_kernel<true>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, nmb, m);
+        else hipLaunchKernelGGL(prep_kernel<false>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, nmb, m);
+    } else {
+        hipLaunchKernelGGL(mask_rows_kernel, dim3(nmb), dim3(256), 0, st, m);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStream_t st) {
     using namespace pp;
     const int nqg = (a.nq + BM - 1) / BM;
@@ -945,27 +966,12 @@ hipError_t launch_prefill64_pp(const AttnArgs& a, const StageReq* stage, hipStre
     const GridMap gm = (a.mask || a.im_causal) ? GridMap::make_tiles_desc((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk)
                                                : GridMap::make((int)nwg, nqg, a.hq, a.hkv, a.b, a.bk);
     const dim3 grid((unsigned)nwg), block(NT);
-    StageArgs sa;
-    uint32_t sb = 0;
-    bool snt = false;
-    if (stage && !make_stage_args(*stage, sa, sb, snt)) return hipErrorInvalidValue;
     if (a.mask) {
-        if (!a.mask_rows) return hipErrorInvalidValue;
-        const int64_t nrows = (int64_t)a.nq * a.hm * a.bm;
-        if (nrows > 0x7fffffff - 15) return hipErrorInvalidValue;
-        const MaskRowArgs m{a.mask, a.m_nb1, a.m_nb2, a.m_nb3, a.nkv, a.nq, a.hm, (int)nrows, a.mask_rows};
-        const uint32_t nmb = (uint32_t)((nrows + 3) / 4);   // four rows per block
-        if (sb > 0) {
-            const uint64_t nb = 2ull * sb + nmb;
-            if (nb > 0x7fffffffull) return hipErrorInvalidValue;
-            if (snt) hipLaunchKernelGGL(prep_kernel<true>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, nmb, m);
-            else hipLaunchKernelGGL(prep_kernel<false>, dim3((unsigned)nb), dim3(256), 0, st, sa, sb, nmb, m);
-        } else {
-            hipLaunchKernelGGL(mask_rows_kernel, dim3(nmb), dim3(256), 0, st, m);
-        }
+        const hipError_t e = launch_mask_prep(a, stage, st);
+        if (e != hipSuccess) return e;
         launch_pp_mm<1>(a, gm, nblk, ni, is_c8, grid, block, st);
     } else {
-        if (sb > 0) {
+        if (stage) {
             const hipError_t e = launch_to_f16_kv(*stage, st);
             if (e != hipSuccess) return e;
         }

@@ -36,11 +36,16 @@ struct Tuning {
     bool pp_enabled = true;
     // VXFA_PREFILL_PAIR=0 routes short masked hd 128 prefill to the general kernel
     bool pair_enabled = true;
+    // VXFA_PAIR_INTERVALS=0: with F32 K/V and a mask tensor the short masked
+    // prefill classifies its blocks from the mask itself rather than from the
+    // intervals a pre-pass finds in the staging launch
+    bool pair_intervals = true;
     void read_env() {
         if (const char* e = getenv("VXFA_DECODE_SPLIT")) split_override = atoi(e);
         if (const char* e = getenv("VXFA_PREFILL_WAVES")) waves_override = atoi(e);
         if (const char* e = getenv("VXFA_PREFILL_PP")) pp_enabled = atoi(e) != 0;
         if (const char* e = getenv("VXFA_PREFILL_PAIR")) pair_enabled = atoi(e) != 0;
+        if (const char* e = getenv("VXFA_PAIR_INTERVALS")) pair_intervals = atoi(e) != 0;
     }
 };
 
@@ -513,20 +518,20 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             a.k_nb3 = a.v_nb3 = Nkv * Hkv * D * 2;
             a.kv_f32 = 0;
         }
-        // a mask tensor on the pipelined hd 64 kernel: the live interval of
-        // each mask row (8 bytes a row) in the records region, unused by a
-        // prefill call; where records and staging share one area (the no-alloc
+        // a mask tensor with a pre-pass (the pipelined hd 64 kernel; the short
+        // masked prefill when F32 K/V are staged): the live interval of each
+        // mask row (8 bytes a row) in the records region, unused by a prefill
+        // call; where records and staging share one area (the no-alloc
         // scratch), after the staged K/V
-        bool pp_mask_fits = false;
+        int2* mrows = nullptr;
         if (mask) {
             const size_t off = w.rec == reinterpret_cast<float*>(w.stage) ? (staged + 255) & ~(size_t)255 : 0;
             const size_t need = (size_t)(Nq * a.hm * a.bm) * sizeof(int2);
-            if (off + need <= w.rec_bytes) {
-                a.mask_rows = reinterpret_cast<int2*>(reinterpret_cast<char*>(w.rec) + off);
-                pp_mask_fits = true;
-            }
+            if (off + need <= w.rec_bytes) mrows = reinterpret_cast<int2*>(reinterpret_cast<char*>(w.rec) + off);
         }
+        const bool pp_mask_fits = mrows != nullptr;
         if (D == 64 && (!mask || pp_mask_fits) && !rope && scale != 0.0f && w.tune.pp_enabled) {
+            a.mask_rows = mrows;
             // (scale 0 goes to the general kernel: the pipelined one folds the
             // scale into the exponent and scores the partial block's dead rows -inf)
             // encoder prefill: the software-pipelined hd 64 kernel, also under
@@ -535,11 +540,22 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             // pre-pass's launch when there is one
             e = vxfa::launch_prefill64_pp(a, staged ? &stage : nullptr, st);
         } else {
+            const bool pair = D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled &&
+                              vxfa::prefill_pair_fits(a);
+            if (pair && staged && mask && mrows && w.tune.pair_intervals) {
+                // the decoder prefill as voxtral calls it (F32 cache, F16 mask):
+                // the staging launch also finds the mask rows' intervals, from
+                // which the short masked prefill takes its block classes
+                a.mask_rows = mrows;
+                e = vxfa::launch_mask_prep(a, &stage, st);
+                if (e != hipSuccess) { set_err(w, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
+                staged = 0;   // (done in that launch)
+            }
             if (staged) {
                 e = vxfa::launch_to_f16_kv(stage, st);
                 if (e != hipSuccess) { set_err(w, "F32 K/V staging: %s", hipGetErrorString(e)); return VXFA_HIP_ERROR; }
             }
-            if (D == 128 && (mask || implicit) && Nkv <= 512 && w.tune.pair_enabled && vxfa::prefill_pair_fits(a)) {
+            if (pair) {
                 // short masked prefill (voxtral's decoder prefill): paired query
                 // tiles, every live block on its own wavefront
                 e = vxfa::launch_prefill_pair(a, st);
