@@ -36,6 +36,7 @@ struct AttnArgs {
     int32_t q_f16;        // q element type is f16
     int32_t kv_f32;       // k and v element type is F32 (else f16)
     int32_t n_split;      // decode: workgroups per (batch, kv head)
+    int32_t dec_t16;      // decode, f16 K/V: 16-position tiles (short spans) instead of 32
     int32_t mask_vec;     // mask data and strides 16-byte aligned (128-bit mask loads)
     float scale_log2;     // scale * log2(e)
     // implicit causal / window mask (instead of a mask tensor): query row i

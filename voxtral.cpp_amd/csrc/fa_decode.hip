@@ -32,8 +32,9 @@
 // fence writes back and invalidates the whole L2 of its XCD).
 //
 // Inside a wavefront (tiles of TP positions, 32 for f16 and 16 for F32 K/V,
-// so a tile is 16 KB either way; software pipelined: the next tile's K/V
-// loads are in flight while the current tile is computed):
+// so a tile is 16 KB either way, and 16 for f16 on short spans, where tiles
+// of 32 would leave the grid short of workgroups; software pipelined: the
+// next tile's K/V loads are in flight while the current tile is computed):
 //   QK^T  v_mfma_f32_16x16x32_f16 per (16 positions, 32 dims); against F32
 //         K, v_mfma_f32_16x16x4f32 per (16 positions, 4 dims) with F32 Q.
 //         The A operand holds the G query heads replicated 16/G times, so
@@ -161,12 +162,15 @@ struct DecodeDivs {
 
 // two wavefronts per SIMD (256 registers per lane, arch + accumulation): the
 // masked f16 variant otherwise took 256 + 2 and ran one per SIMD
-template <int D, int G, bool QF16, bool MASK, bool KV32, bool RING>
+template <int D, int G, bool QF16, bool MASK, bool KV32, bool RING, bool T16>
 __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDivs dv) {
     static_assert(D == 64 || D == 128, "head dim");
     static_assert(G == 1 || G == 2 || G == 4, "GQA group");
     constexpr int KS = D / 32;        // MFMA k-steps of 32 dims
-    constexpr int TP = KV32 ? 16 : 32;   // positions per tile (16 KB of K and V either way)
+    // positions per tile: 32 for f16 K/V (16 KB of K and V), 16 for F32 (16 KB)
+    // and for f16 on short spans (T16: twice the workgroups for the same span)
+    constexpr int TP = (KV32 || T16) ? 16 : 32;
+    static_assert(!(KV32 && T16), "F32 tiles are 16 positions already");
     constexpr int NG = TP / 16;       // 16-position MFMA groups per tile
     constexpr int CH = D / 8;         // lanes per V row (8 dims each)
     constexpr int RPI = 64 / CH;      // V rows covered by one load instruction
@@ -729,23 +733,23 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
     }
 }
 
-template <int D, int G, bool KV32>
+template <int D, int G, bool KV32, bool T16>
 static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
     const dim3 grid(a.n_split * a.hkv, a.b), block(DEC_THREADS);
     const DecodeDivs dv = {DivMod::make(a.hkv), DivMod::make(a.n_split), DivMod::make(a.b / a.bk),
                            DivMod::make(a.hm > 0 ? a.hm : 1), DivMod::make(a.bm > 0 ? a.bm : 1)};
     if (a.mask) {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32, false>), grid, block, 0, st, a, dv);
-        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32, false>), grid, block, 0, st, a, dv);
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, true, KV32, false, T16>), grid, block, 0, st, a, dv);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, true, KV32, false, T16>), grid, block, 0, st, a, dv);
     } else if (a.ring_cap > 0) {
         // a ring: f16 cache, no mask tensor (the host rejects anything else)
         if constexpr (!KV32) {
-            if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, false, true>), grid, block, 0, st, a, dv);
-            else hipLaunchKernelGGL((fa_decode<D, G, false, false, false, true>), grid, block, 0, st, a, dv);
+            if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, false, true, T16>), grid, block, 0, st, a, dv);
+            else hipLaunchKernelGGL((fa_decode<D, G, false, false, false, true, T16>), grid, block, 0, st, a, dv);
         }
     } else {
-        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32, false>), grid, block, 0, st, a, dv);
-        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32, false>), grid, block, 0, st, a, dv);
+        if (a.q_f16) hipLaunchKernelGGL((fa_decode<D, G, true, false, KV32, false, T16>), grid, block, 0, st, a, dv);
+        else hipLaunchKernelGGL((fa_decode<D, G, false, false, KV32, false, T16>), grid, block, 0, st, a, dv);
     }
     // the combine loads ceil(n_split / 8) partial slices per lane
     const dim3 cgrid(a.hkv * G * (D / 32), a.b);
@@ -755,10 +759,10 @@ static hipError_t launch_dgk(const AttnArgs& a, hipStream_t st) {
     else if (a.n_split > 1) hipLaunchKernelGGL((fa_decode_combine<D, G, 1>), cgrid, dim3(64), 0, st, a);
     return hipGetLastError();
 }
-
 template <int D, int G>
 static hipError_t launch_dg(const AttnArgs& a, hipStream_t st) {
-    return a.kv_f32 ? launch_dgk<D, G, true>(a, st) : launch_dgk<D, G, false>(a, st);
+    if (a.kv_f32) return launch_dgk<D, G, true, false>(a, st);
+    return a.dec_t16 ? launch_dgk<D, G, false, true>(a, st) : launch_dgk<D, G, false, false>(a, st);
 }
 
 hipError_t launch_decode(const AttnArgs& a, int head_dim, int group, hipStream_t st) {

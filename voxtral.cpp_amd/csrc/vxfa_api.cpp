@@ -251,11 +251,24 @@ vxfa::AppendArgs append_args(const vxfa_tensor* k, const vxfa_tensor* v, const v
 // 11.30 (64); 8192 12.25 (64) against 12.99 (32). With a mask tensor every
 // split workgroup scans the whole mask row, so the caller caps the count
 // (measured on a 2048 window of a 16K cache).
-int choose_split(int64_t pairs, int64_t nkv, bool kv_f32) {
+// Split count of a decode call: about 2048 wavefronts in all, at least one
+// tile per wavefront. f16 tiles hold 32 positions, F32 tiles 16; *t16 is set
+// when f16 tiles of 32 would leave fewer workgroups than the target (short
+// spans: n_kv 1024, a 2048 window), and the tiles then hold 16 positions
+// too (twice the workgroups for the span: n_kv 1024 7.01 -> 6.55 us, a
+// 2048-row ring with append 8.61 -> 7.67; at n_kv 8192, where tiles of 32
+// already fill the grid, tiles of 16 measured slower, 10.96 -> 12.07).
+int choose_split(int64_t pairs, int64_t nkv, bool kv_f32, bool* t16) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
-    const int64_t per = (int64_t)vxfa::kDecodeWaves * (kv_f32 ? 16 : 32);   // one tile per wavefront
-    const int64_t by_len = (nkv + per - 1) / per;
+    int64_t per = (int64_t)vxfa::kDecodeWaves * (kv_f32 ? 16 : 32);   // one tile per wavefront
+    int64_t by_len = (nkv + per - 1) / per;
+    *t16 = false;
+    if (!kv_f32 && by_len < s) {
+        *t16 = true;
+        per = (int64_t)vxfa::kDecodeWaves * 16;
+        by_len = (nkv + per - 1) / per;
+    }
     if (s > by_len) s = by_len;
     if (s > vxfa::kDecodeMaxSplit) s = vxfa::kDecodeMaxSplit;
     if (s < 1) s = 1;
@@ -474,7 +487,13 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
             a.kv_hi = (int32_t)hi;
             a.im_causal = 0;   // the range is all the decode kernel needs
         }
-        int S = choose_split(B * Hkv, a.kv_hi - a.kv_lo, a.kv_f32 != 0);
+        bool t16 = false;
+        int S = choose_split(B * Hkv, a.kv_hi - a.kv_lo, a.kv_f32 != 0, &t16);
+        // one mask row (a sliding window over a longer cache): the live span,
+        // which sets the tiles per split, is found by the kernel; tiles of 16
+        // keep every wavefront busy on a window's share (2048 of 16384 rows in
+        // 32 splits: 10.29 -> 9.83 us)
+        if (mask && B == 1 && !a.kv_f32) t16 = true;
         if (mask && B > 1) {
             // streams of ragged lengths (a mask row each): the longest sets the
             // time, so split every stream finer, about 2048 workgroups in all
@@ -486,6 +505,7 @@ int run(Workspace& w, const vxfa_tensor* q, const vxfa_tensor* k, const vxfa_ten
         if (S > vxfa::kDecodeMaxSplit) S = vxfa::kDecodeMaxSplit;
         S = fit_split(S, B * Hkv, vxfa::dec_record_floats((int)D, (int)G), w.rec_bytes);
         a.n_split = S;
+        a.dec_t16 = t16 ? 1 : 0;
         a.ws = w.rec;
         e = vxfa::launch_decode(a, (int)D, (int)G, st);
     } else {
