@@ -49,7 +49,9 @@ def test_noalloc_batched_then_single(runner):
 
 def test_noalloc_prefill_and_f32_staging(runner):
     """Causal prefill (no scratch), F32 encoder K/V (7.7 MB of f16 staging in
-    the scratch), then a smaller F32 prefill."""
+    the scratch), then a smaller F32 causal prefill (the short masked prefill
+    whose mask row intervals, found in the staging launch, sit in the scratch
+    after the staged K/V)."""
     _same(runner, cases.prefill_case(439, seed=305))
     _same(runner, cases.encoder_case(1500, 20, 64, seed=306, kv_f32=True))
     _same(runner, cases.prefill_case(100, seed=307, kv_f32=True))
