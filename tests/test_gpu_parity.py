@@ -974,6 +974,25 @@ def test_f32_prefill_interval_classes_bitwise(runner, n, nkv):
     assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
 
 
+def test_f32_prefill_intervals_with_f16_q(runner):
+    """F16 Q on the interval route (the pair kernel's F16-Q instantiation):
+    a causal prefill after 100 cached rows with F32 K/V, the same bits as
+    classifying from the mask, within the bar of the oracle."""
+    n, off = 139, 100
+    c = cases.prefill_case(n, seed=1600, kv_offset=off, kv_f32=True)
+    q = c.bufs["q"].reshape(n, 32, 128).astype(np.float32)
+    c.bufs["q"] = cases.f16_bits(q)
+    c.views["q"] = ("q", oracle.F16, *cases.views.decoder_q(n, 32, 128, 2), 0)
+    out = check_case(runner, c)
+    other = _runner_with_env(VXFA_PAIR_INTERVALS=0)
+    try:
+        rc, out2 = other.run(c)
+        assert rc == 0
+    finally:
+        other.close()
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+
+
 @pytest.mark.parametrize("kind", ["sparse", "bias", "empty_rows", "window"])
 def test_f32_prefill_masks_through_intervals(runner, kind):
     """Masks whose rows are not all intervals take the fallback (every block
