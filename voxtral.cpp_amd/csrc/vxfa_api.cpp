@@ -251,13 +251,13 @@ vxfa::AppendArgs append_args(const vxfa_tensor* k, const vxfa_tensor* v, const v
 // 11.30 (64); 8192 12.25 (64) against 12.99 (32). With a mask tensor every
 // split workgroup scans the whole mask row, so the caller caps the count
 // (measured on a 2048 window of a 16K cache).
-// Split count of a decode call: about 2048 wavefronts in all, at least one
-// tile per wavefront. f16 tiles hold 32 positions, F32 tiles 16; *t16 is set
-// when f16 tiles of 32 would leave fewer workgroups than the target (short
-// spans: n_kv 1024, a 2048 window), and the tiles then hold 16 positions
-// too (twice the workgroups for the span: n_kv 1024 7.01 -> 6.55 us, a
-// 2048-row ring with append 8.61 -> 7.67; at n_kv 8192, where tiles of 32
-// already fill the grid, tiles of 16 measured slower, 10.96 -> 12.07).
+// Tile size: *t16 is set when f16 tiles of 32 positions would leave fewer
+// workgroups than the target (short spans: n_kv 1024, a 2048 window); the
+// tiles then hold 16 positions, as F32 tiles do, and the split count doubles
+// for the same span (n_kv 1024 7.01 -> 6.55 us per layer, a 2048-row ring
+// with append 8.61 -> 7.67; at n_kv 8192, where tiles of 32 already fill the
+// grid, tiles of 16 measured slower, 10.96 -> 12.07, and tiles of 8 on short
+// spans gained nothing at 1024 and lost 0.4-0.8 us on the 2048 window).
 int choose_split(int64_t pairs, int64_t nkv, bool kv_f32, bool* t16) {
     const int64_t target = 2048 / vxfa::kDecodeWaves;
     int64_t s = (target + pairs - 1) / pairs;
