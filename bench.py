@@ -324,15 +324,15 @@ def _cpu_inputs(kind, seed):
 
 
 # configuration -> (input kind, calls timed per repetition, repetitions);
-# about 10 s of CPU work in all at 16 threads
+# about 10-11 s of CPU work in all at 16 threads (both thread counts)
 CPU_SAMPLES = {
-    "encoder_prefill_1500x20_hd64": ("encoder", 1, 41),
-    "realtime_encoder_1500x32_hd64_w750": ("realtime", 1, 21),
+    "encoder_prefill_1500x20_hd64": ("encoder", 1, 61),
+    "realtime_encoder_1500x32_hd64_w750": ("realtime", 1, 41),
     "decode_nkv1024": ("decode1024", 50, 41),
     "decode_nkv8192": ("decode8192", 5, 61),
     "decoder_prefill_439_causal": ("prefill439", 1, 61),
     "sliding_window_decode_16k_w2048": ("sliding", 20, 41),
-    "batched_ragged_32_streams": ("batched", 1, 41),
+    "batched_ragged_32_streams": ("batched", 1, 61),
 }
 
 
@@ -758,7 +758,7 @@ def main():
         cpu = {"value": flops_enc / (enc_us * 1e-6) / 1e12, "unit": "TFLOP/s", "cores": t_def, "kind": "port",
                "sample": "every configuration: encoder 1500x20 hd64 (one layer), realtime encoder 1500x32 hd64 "
                          "window 750, decode n_kv 1024 and 8192, decoder prefill 439 causal, one sliding-window "
-                         "step (n_kv 16335, window 2048), the 32-stream ragged batch; median of 21-61 repetitions "
+                         "step (n_kv 16335, window 2048), the 32-stream ragged batch; median of 41-61 repetitions "
                          "per configuration and thread count through oracle/fa_cpu_simd.c (ggml's one-row "
                          "algorithm with AVX2/F16C vector kernels, f16 V accumulation), "
                          f"{total:.1f} s of CPU work",
