@@ -315,10 +315,12 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
         const int r = pos + a.ring_start;
         return r >= a.ring_cap ? r - a.ring_cap : r;
     };
-    // f16 K/V tiles are read once per step: nontemporal loads without a mask
-    // tensor (measured 12.65 -> 12.37 us per layer at n_kv 8192 on one box,
-    // 12.66 -> 12.60 on another); with one (the ragged batch) and for the F32
-    // cache they measured ~1 % slower, so those keep ordinary loads
+    // K/V tiles are read once per step: nontemporal loads without a mask
+    // tensor (f16, measured 12.65 -> 12.37 us per layer at n_kv 8192 on one
+    // box, 12.66 -> 12.60 on another; F32 with 16-position tiles and F32
+    // MFMA, 19.4 -> 18.7 us, which also leaves the split records in L2 for
+    // the combine); with one (the ragged batch) they measured ~1 % slower,
+    // so masked f16 tiles keep ordinary loads
     // Addresses: a wave-uniform 64-bit row base (scalar registers) plus a
     // 32-bit lane offset, row * stride + column bytes by one 24-bit
     // multiply-add (the host keeps strides and ring sizes below 2^24 and a
@@ -352,8 +354,8 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
         for (int i = 0; i < NV; ++i) {
             const char* kp = ktile + row_off(vrow + i * RPI, knb, vcol * ESZ);
             if constexpr (KV32) {
-                T.k[i][0] = *(const floatx4*)(kp);
-                T.k[i][1] = *(const floatx4*)(kp + 16);
+                T.k[i][0] = __builtin_nontemporal_load((const floatx4*)(kp));
+                T.k[i][1] = __builtin_nontemporal_load((const floatx4*)(kp + 16));
             } else if constexpr (masked) {
                 T.k[i] = *(const half8*)(kp);
             } else {
@@ -372,8 +374,8 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
         for (int i = 0; i < NV; ++i) {
             const char* vp = vt + row_off(vrow + i * RPI, vnb, vcol * ESZ);
             if constexpr (KV32) {
-                T.v[i][0] = *(const floatx4*)(vp);
-                T.v[i][1] = *(const floatx4*)(vp + 16);
+                T.v[i][0] = __builtin_nontemporal_load((const floatx4*)(vp));
+                T.v[i][1] = __builtin_nontemporal_load((const floatx4*)(vp + 16));
             } else if constexpr (masked) {
                 T.v[i] = *(const half8*)(vp);
             } else {
