@@ -318,9 +318,9 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void fa_decode(AttnArgs a, DecodeDi
     // K/V tiles are read once per step: nontemporal loads without a mask
     // tensor (f16, measured 12.65 -> 12.37 us per layer at n_kv 8192 on one
     // box, 12.66 -> 12.60 on another; F32 with 16-position tiles and F32
-    // MFMA, 19.4 -> 18.7 us, which also leaves the split records in L2 for
-    // the combine); with one (the ragged batch) they measured ~1 % slower,
-    // so masked f16 tiles keep ordinary loads
+    // MFMA, 19.4 -> 18.7 us, likely also by leaving the split records in L2
+    // for the combine); with one (the ragged batch) they measured ~1 %
+    // slower, so masked f16 tiles keep ordinary loads
     // Addresses: a wave-uniform 64-bit row base (scalar registers) plus a
     // 32-bit lane offset, row * stride + column bytes by one 24-bit
     // multiply-add (the host keeps strides and ring sizes below 2^24 and a
