@@ -895,7 +895,8 @@ F32_ATOL, F32_RTOL = 2e-5, 1e-4
 
 
 @pytest.mark.parametrize("n_kv,hd,groups,q_f16", [(1024, 128, 4, False), (8192, 128, 4, False), (3000, 64, 2, False),
-                                                  (700, 128, 1, False), (1024, 128, 4, True)])
+                                                  (700, 128, 1, False), (1024, 128, 4, True), (2048, 64, 4, False),
+                                                  (517, 128, 2, False), (33, 64, 1, True), (1, 128, 4, False)])
 def test_f32_cache_decode_keeps_f32_products(runner, n_kv, hd, groups, q_f16):
     import gpu_util
     c = cases.decode_case(n_kv, hq=8 * groups, hkv=8, hd=hd, seed=1300 + n_kv + hd, kv_f32=True, q_f16=q_f16)
