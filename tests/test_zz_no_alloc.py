@@ -42,6 +42,13 @@ def test_noalloc_decode_then_smaller_decode(runner):
     _same(runner, cases.decode_case(1000, seed=302), oracle=True)
 
 
+def test_noalloc_f32_cache_decode(runner):
+    """The reference's F32 cache (F32 products, its split records in the
+    scratch): n_kv 8192, then an hd 64 call with fewer splits."""
+    _same(runner, cases.decode_case(8192, seed=317, kv_f32=True), oracle=True)
+    _same(runner, cases.decode_case(700, hq=16, hkv=8, hd=64, seed=318, kv_f32=True), oracle=True)
+
+
 def test_noalloc_batched_then_single(runner):
     _same(runner, cases.batched_case(16, capacity=2048, lo=100, hi=2048, seed=303))
     _same(runner, cases.decode_case(333, hq=16, hkv=8, hd=64, seed=304))
